@@ -1,0 +1,279 @@
+"""Benchmark: find and insert_or_assign on one MI355X.
+
+Workload (the headline lookup/upsert shape): kLru table, capacity 2^26 slots
+in 128-slot buckets, dim 64 fp32 values all in HBM, batches of 2^20
+uniform-random uint64 keys.  One step = insert_or_assign of one batch of new
+keys + find of one batch of resident keys (100% hit).  The table is filled
+so that the load factor crosses 0.5 in the middle of the timed steps.
+Inputs are resident in HBM before timing starts.
+
+Prints one JSON line.  Also reported: insert_or_assign at load factors 0.75
+and 1.0, find at 0% hit (plain and missed-keys overload), and the host
+reference (the oracle) timed on a bounded sample of the same workload.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "hierarchicalkv-ascend_amd"))
+
+METRIC = ("find & insert_or_assign Mkeys/s at cap 64M dim 64, lf 0.5/1.0; "
+          "% HBM peak")
+HBM_PEAK_GBS = 8000.0
+S = 64          # bytes charged per random touch of bucket metadata
+CAP = 1 << 26
+DIM = 64
+BATCH = 1 << 20
+
+
+def algo_bytes(op, dim=DIM):
+    """Algorithmic bytes per key (fixed model: S per random metadata touch,
+    x2 when read-modify-write; V = 4*dim per row direction)."""
+    V = 4 * dim
+    return {
+        "find_hit": 9 + 2 * S + 2 * V,
+        "find_miss": 9 + S,
+        "insert_new": 8 + 2 * V + 8 * S,
+        "insert_evict": 8 + 2 * V + 8 * S + 2048,
+    }[op]
+
+
+def rand_keys(torch, n, gen):
+    k = torch.randint(-(2**63), 2**63 - 1, (n,), dtype=torch.int64,
+                      device="cuda", generator=gen)
+    # Reserved keys are 0xFFFFFFFFFFFFFFFC..FF (-4..-1 as int64).
+    bad = (k >= -4) & (k < 0)
+    return torch.where(bad, k - 4, k)
+
+
+def cpu_baseline(seconds_hint=20.0):
+    """The oracle on the host cores: kLru, capacity 2^26, dim 64, filled to
+    load factor ~0.5, then insert_or_assign of new keys and find of resident
+    keys in 2^20-key batches."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+    import oracle as O
+    threads = min(16, os.cpu_count() or 1)
+    t = O.Oracle(CAP, dim=DIM, strategy=O.LRU, threads=threads)
+    rng = np.random.default_rng(7)
+    resident = []
+    vals = rng.uniform(-1, 1, (BATCH, DIM)).astype(np.float32)
+    clk = 1
+    for b in range(30):  # fill to ~0.47
+        ks = rng.integers(0, 2**62, BATCH, dtype=np.uint64)
+        t.insert_or_assign(ks, vals, clock=clk)
+        clk += 1
+        resident.append(ks)
+    resident = np.concatenate(resident)
+    n_ins = n_find = 0
+    t_ins = t_find = 0.0
+    t_start = time.perf_counter()
+    while time.perf_counter() - t_start < seconds_hint and n_ins < 8 * BATCH:
+        ks = rng.integers(0, 2**62, BATCH, dtype=np.uint64)
+        q = rng.choice(resident, BATCH)
+        a = time.perf_counter()
+        t.insert_or_assign(ks, vals, clock=clk)
+        b_ = time.perf_counter()
+        t.find(q)
+        c = time.perf_counter()
+        clk += 1
+        t_ins += b_ - a
+        t_find += c - b_
+        n_ins += BATCH
+        n_find += BATCH
+    val = (n_ins + n_find) / (t_ins + t_find) / 1e6
+    return {"value": round(val, 3), "unit": "Mkeys/s", "cores": threads,
+            "kind": "port",
+            "sample": ("oracle, kLru cap 2^26 dim 64 at load factor ~0.5: "
+                       f"{n_ins // BATCH} insert_or_assign + {n_find // BATCH} "
+                       "find batches of 2^20 keys, bucket-partitioned threads"),
+            "insert_mkeys_s": round(n_ins / t_ins / 1e6, 3),
+            "find_mkeys_s": round(n_find / t_find / 1e6, 3)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=8)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the load factor 0.75/1.0 and miss points")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: the table is a single-device "
+              "structure here (multi-GPU sharding is a design note, not a "
+              "measured path). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import hkv_amd
+
+    K, W = args.steps, args.warmup
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.Stream(device=dev)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(1234)
+    table = hkv_amd.HashTable("u64", "f32", hkv_amd.EvictStrategy.kLru)
+    table.init(hkv_amd.HashTableOptions(
+        init_capacity=CAP, max_capacity=CAP,
+        max_hbm_for_vectors=CAP * DIM * 4, dim=DIM))
+    values = torch.rand((BATCH, DIM), dtype=torch.float32, device=dev,
+                        generator=gen) * 2 - 1
+    out_vals = torch.empty((BATCH, DIM), dtype=torch.float32, device=dev)
+    founds = torch.empty(BATCH, dtype=torch.uint8, device=dev)
+    batches_to_half = (CAP // 2) // BATCH
+    fill = batches_to_half - W - K // 2
+    resident = []
+    with torch.cuda.stream(stream):
+        for _ in range(fill):
+            ks = rand_keys(torch, BATCH, gen)
+            table.insert_or_assign(BATCH, ks, values, None, stream)
+            resident.append(ks)
+        # Inputs of warmup and timed steps, generated before timing.
+        ins_keys = [rand_keys(torch, BATCH, gen) for _ in range(W + K)]
+        res_all = torch.cat(resident)
+        find_keys = [res_all[torch.randint(0, res_all.numel(), (BATCH,),
+                                           device=dev, generator=gen)]
+                     for _ in range(W + K)]
+    torch.cuda.synchronize()
+    lf_start = None
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)]
+          for _ in range(K)]
+    with torch.cuda.stream(stream):
+        for s in range(W):
+            table.insert_or_assign(BATCH, ins_keys[s], values, None, stream)
+            table.find(BATCH, find_keys[s], out_vals, founds, None, stream)
+        torch.cuda.synchronize()
+        lf_start = table.load_factor(stream)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for s in range(K):
+            e = ev[s]
+            e[0].record(stream)
+            table.insert_or_assign(BATCH, ins_keys[W + s], values, None, stream)
+            e[1].record(stream)
+            table.find(BATCH, find_keys[W + s], out_vals, founds, None, stream)
+            e[2].record(stream)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+    lf_end = table.load_factor(stream)
+    hit = int(founds.sum().item())
+    ins_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / K
+    find_ms = sum(e[1].elapsed_time(e[2]) for e in ev) / K
+    wall = t1 - t0
+    value = 2 * BATCH * K / wall / 1e6
+
+    def gbs(op, ms):
+        return algo_bytes(op) * BATCH / (ms * 1e-3) / 1e9
+
+    ins_gbs = gbs("insert_new", ins_ms)
+    find_gbs = gbs("find_hit", find_ms)
+    breakdown = {
+        "insert_or_assign_lf0.5": {
+            "mkeys_s": round(BATCH / ins_ms / 1e3, 1), "ms": round(ins_ms, 4),
+            "algo_gbs": round(ins_gbs, 1),
+            "frac_hbm": round(ins_gbs / HBM_PEAK_GBS, 4),
+            "bytes_per_key": algo_bytes("insert_new")},
+        "find_hit_lf0.5": {
+            "mkeys_s": round(BATCH / find_ms / 1e3, 1), "ms": round(find_ms, 4),
+            "algo_gbs": round(find_gbs, 1),
+            "frac_hbm": round(find_gbs / HBM_PEAK_GBS, 4),
+            "bytes_per_key": algo_bytes("find_hit"), "hits": hit},
+        "load_factor_range": [round(lf_start, 4), round(lf_end, 4)],
+    }
+
+    if not args.no_extra:
+        with torch.cuda.stream(stream):
+            def time_op(fn, reps=3):
+                es = [torch.cuda.Event(enable_timing=True) for _ in range(2 * reps)]
+                for r in range(reps):
+                    es[2 * r].record(stream)
+                    fn(r)
+                    es[2 * r + 1].record(stream)
+                torch.cuda.synchronize()
+                return sum(es[2 * r].elapsed_time(es[2 * r + 1])
+                           for r in range(reps)) / reps
+            miss_keys = rand_keys(torch, BATCH, gen)
+            fm_ms = time_op(lambda r: table.find(BATCH, miss_keys, out_vals,
+                                                 founds, None, stream))
+            mk = torch.empty(BATCH, dtype=torch.int64, device=dev)
+            mi = torch.empty(BATCH, dtype=torch.int32, device=dev)
+            ms_ = torch.empty(1, dtype=torch.int32, device=dev)
+            fmm_ms = time_op(lambda r: table.find_missed(
+                BATCH, miss_keys, out_vals, mk, mi, ms_, None, stream))
+            breakdown["find_miss_lf0.5"] = {
+                "mkeys_s": round(BATCH / fm_ms / 1e3, 1), "ms": round(fm_ms, 4),
+                "algo_gbs": round(gbs("find_miss", fm_ms), 1)}
+            breakdown["find_missed_overload_lf0.5"] = {
+                "mkeys_s": round(BATCH / fmm_ms / 1e3, 1), "ms": round(fmm_ms, 4)}
+            for target, name, model in ((0.75, "insert_or_assign_lf0.75", "insert_new"),
+                                        (1.0, "insert_or_assign_lf1.0", "insert_evict")):
+                guard = 0
+                while table.load_factor(stream) < target - 1e-9 and guard < 200:
+                    lf = table.load_factor(stream)
+                    if target < 1.0 and lf + BATCH / CAP > target:
+                        break
+                    table.insert_or_assign(BATCH, rand_keys(torch, BATCH, gen),
+                                           values, None, stream)
+                    guard += 1
+                lf0 = table.load_factor(stream)
+                nk = [rand_keys(torch, BATCH, gen) for _ in range(3)]
+                torch.cuda.synchronize()
+                t_ms = time_op(lambda r: table.insert_or_assign(
+                    BATCH, nk[r], values, None, stream))
+                g = gbs(model, t_ms)
+                breakdown[name] = {
+                    "mkeys_s": round(BATCH / t_ms / 1e3, 1), "ms": round(t_ms, 4),
+                    "algo_gbs": round(g, 1), "frac_hbm": round(g / HBM_PEAK_GBS, 4),
+                    "load_factor_at_start": round(lf0, 4)}
+            hf = time_op(lambda r: table.find(BATCH, nk[r], out_vals, founds,
+                                              None, stream))
+            breakdown["find_hit_lf1.0"] = {"mkeys_s": round(BATCH / hf / 1e3, 1),
+                                           "ms": round(hf, 4)}
+
+    # The dominant operation of the step sets the roofline line.
+    if ins_ms >= find_ms:
+        roof = {"kernel": "insert_or_assign (route + apply kernels)",
+                "achieved": round(ins_gbs, 1), "bytes_per_key": algo_bytes("insert_new"),
+                "ms_per_launch": round(ins_ms, 4)}
+    else:
+        roof = {"kernel": "find", "achieved": round(find_gbs, 1),
+                "bytes_per_key": algo_bytes("find_hit"),
+                "ms_per_launch": round(find_ms, 4)}
+    roofline = {"bound": "hbm", "achieved": roof["achieved"], "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(roof["achieved"] / HBM_PEAK_GBS, 4),
+                "traffic": None, "kernel": roof["kernel"],
+                "keys_per_launch": BATCH, "bytes_per_key": roof["bytes_per_key"],
+                "ms_per_launch": roof["ms_per_launch"]}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        try:
+            cpu = cpu_baseline()
+        except Exception as exc:  # reported, never fatal for the GPU line
+            cpu = {"error": repr(exc)}
+
+    line = {
+        "metric": METRIC, "value": round(value, 2), "unit": "Mkeys/s",
+        "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": round(wall / K * 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "u64",
+        "data": "synthetic",
+        "config": {"workload": "kLru cap 2^26 (128-slot buckets) dim 64 fp32 in HBM, "
+                               "2^20-key batches: insert_or_assign new keys + find "
+                               "resident keys around load factor 0.5",
+                   "capacity": CAP, "dim": DIM, "batch": BATCH,
+                   "strategy": "kLru", "parallelism": "single GPU"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "breakdown": breakdown,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

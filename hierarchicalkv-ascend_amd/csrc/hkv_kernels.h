@@ -1,0 +1,74 @@
+// hkv_kernels.h -- host launchers of the gfx950 table kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "hkv_dev.h"
+
+namespace hkv {
+
+// Operations served by the bucket-owner apply path.
+enum ApplyOp {
+  OP_INSERT_OR_ASSIGN = 0,
+  OP_FIND_OR_INSERT = 1,
+  OP_INSERT_AND_EVICT = 2,
+  OP_ACCUM_OR_ASSIGN = 3,
+  OP_ASSIGN_SCORES = 4,
+};
+
+// Eviction tie-break family: the reference's 16-lane digest kernels (unique
+// keys) or its 32-lane find_and_lock tiles (non-unique keys, accum_or_assign).
+enum EvictRule { RULE_DIGEST16 = 0, RULE_TILE32 = 1 };
+
+struct ApplyArgs {
+  const uint64_t* keys;
+  const uint8_t* in_values;   // input rows (deltas for accum)
+  uint8_t* io_values;         // find_or_insert output rows
+  const uint64_t* in_scores;  // may be null
+  const uint8_t* accum_flags; // accum_or_assign only
+  uint64_t* ev_keys;          // insert_and_evict outputs
+  uint8_t* ev_values;
+  uint64_t* ev_scores;
+  uint64_t* ev_counter;
+  uint64_t n;
+  ScoreCtx sc;
+  int rule;
+  int unit;        // row copy unit in bytes
+  int value_type;  // for accumulation
+};
+
+// Per-call scratch of the route/apply pipeline (owned by the table).
+struct RouteScratch {
+  uint32_t* cnt;     // [buckets] keys routed to each bucket, zero between calls
+  uint32_t* pend;    // [buckets * P] batch indices, arrival order
+  uint32_t* heavy;   // [n / (P+1) + 1] buckets with more than P keys
+  uint32_t* ctrl;    // two 64-byte control blocks (ping-pong)
+  uint32_t P;
+};
+
+void launch_init_slots(const TableView& t, uint64_t from_bucket,
+                       uint64_t to_bucket, hipStream_t s);
+void launch_clear(const TableView& t, hipStream_t s);
+void launch_find(const TableView& t, const uint64_t* keys, uint64_t n,
+                 uint8_t* values, uint8_t* founds, uint64_t* scores, int unit,
+                 hipStream_t s);
+void launch_find_missed(const TableView& t, const uint64_t* keys, uint64_t n,
+                        uint8_t* values, uint64_t* missed_keys,
+                        int32_t* missed_idx, int32_t* missed_size,
+                        uint64_t* scores, int unit, hipStream_t s);
+void launch_erase(const TableView& t, const uint64_t* keys, uint64_t n,
+                  hipStream_t s);
+void launch_apply(const TableView& t, int op, const ApplyArgs& a,
+                  RouteScratch& rs, int parity, hipStream_t s);
+void launch_export(const TableView& t, uint64_t offset, uint64_t n,
+                   uint64_t* d_counter, uint64_t* keys, uint8_t* values,
+                   uint64_t* scores, uint32_t* block_scratch, int unit,
+                   hipStream_t s);
+void launch_size(const TableView& t, uint64_t nbuckets, uint64_t* out,
+                 hipStream_t s);
+void launch_rehash(const TableView& t, uint64_t old_buckets, int unit,
+                   hipStream_t s);
+void launch_fill_u64(uint64_t* p, uint64_t v, uint64_t n, hipStream_t s);
+void launch_fill_u32(uint32_t* p, uint32_t v, uint64_t n, hipStream_t s);
+
+}  // namespace hkv

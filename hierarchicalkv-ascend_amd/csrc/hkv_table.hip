@@ -1,0 +1,728 @@
+// hkv_table.hip -- host side of the gfx950 HierarchicalKV table: lifecycle,
+// value slices (HBM or pinned host), argument checks and the C ABI declared
+// in include/hkv_amd.h.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../include/hkv_amd.h"
+#include "hkv_kernels.h"
+
+using namespace hkv;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+struct HkvError {
+  int code;
+  std::string msg;
+};
+
+[[noreturn]] void fail(int code, const std::string& msg) { throw HkvError{code, msg}; }
+
+void hip_check(hipError_t e, const char* what) {
+  if (e != hipSuccess) {
+    fail(HKV_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
+  }
+}
+
+int value_size(int vt) {
+  switch (vt) {
+    case HKV_F32: case HKV_I32: case HKV_U32: return 4;
+    case HKV_F64: case HKV_I64: case HKV_U64: return 8;
+    case HKV_F16: case HKV_BF16: case HKV_I16: case HKV_U16: return 2;
+    case HKV_I8: case HKV_U8: return 1;
+    default: return 0;
+  }
+}
+
+bool ispow2(uint64_t x) { return x && !(x & (x - 1)); }
+
+uint32_t log2_ceil(uint64_t x) {
+  uint32_t s = 0;
+  while ((1ull << s) < x) s++;
+  return s;
+}
+
+// Value slice size (include/table.h:244-268).
+uint64_t ref_slice_bytes(uint64_t max_slots, uint64_t B, uint64_t row) {
+  const uint64_t GB = 1ull << 30, MB = 1ull << 20;
+  const uint64_t min_slice = B * row;
+  const uint64_t tbl = max_slots * row;
+  uint64_t s;
+  if (tbl >= 128 * GB) s = 16 * GB;
+  else if (tbl >= 16 * GB) s = 2 * GB;
+  else if (tbl >= 2 * GB) s = 128 * MB;
+  else if (tbl >= 128 * MB) s = 16 * MB;
+  else if (tbl >= 16 * MB) s = MB;
+  else s = min_slice;
+  return std::max(std::max(min_slice, s), 2 * MB);
+}
+
+struct Slice {
+  uint8_t* host_ptr;  // non-null for pinned host slices
+  uint8_t* dev_ptr;
+  bool hbm;
+};
+
+}  // namespace
+
+struct hkv_table {
+  hkv_options opt{};
+  int key_type = HKV_KEY_U64;
+  int value_type = HKV_F32;
+  int strategy = HKV_LRU;
+  int device = 0;
+  uint64_t B = 128, nb = 0, C = 0, row = 0;
+  uint64_t qd_magic = 0, qd_shift = 0;
+  bool reach_max = false;
+  uint64_t epoch = kIgnoredEpoch;
+  bool clock_override = false;
+  uint64_t clock_value = 0;
+
+  uint8_t* digests = nullptr;
+  uint64_t* keys = nullptr;
+  uint64_t* scores = nullptr;
+  int32_t* bsize = nullptr;
+
+  uint64_t slice_shift = 0;  // buckets per slice = 1 << slice_shift
+  uint64_t remaining_hbm = 0;
+  std::vector<Slice> slices;
+  uint8_t** d_slices = nullptr;
+  size_t d_slices_cap = 0;
+  bool pure_hbm = true;
+
+  // route/apply scratch
+  uint32_t* cnt = nullptr;
+  uint32_t* pend = nullptr;
+  uint64_t pend_cap = 0;  // entries
+  uint32_t* heavy = nullptr;
+  uint64_t heavy_cap = 0;
+  uint32_t* ctrl = nullptr;
+  int parity = 0;
+  // export scratch
+  uint32_t* blk = nullptr;
+  uint64_t blk_cap = 0;
+  // size scratch
+  uint64_t* d_sum = nullptr;
+  uint64_t* h_sum = nullptr;
+
+  TableView view() const {
+    TableView v{};
+    v.digests = digests;
+    v.keys = keys;
+    v.scores = scores;
+    v.bsize = bsize;
+    v.slices = d_slices;
+    v.capacity = C;
+    v.buckets = nb;
+    v.qd_magic = qd_magic;
+    v.qd_shift = qd_shift;
+    v.B = (uint32_t)B;
+    v.bshift = log2_ceil(B);
+    v.slice_shift = (uint32_t)slice_shift;
+    v.row_bytes = (uint32_t)row;
+    v.pow2 = ispow2(C) ? 1u : 0u;
+    return v;
+  }
+
+  void set_capacity(uint64_t c) {
+    C = c;
+    // Divisor precomputation (include/table.h:106-127).
+    unsigned __int128 one = 1;
+    uint64_t s = 0;
+    for (s = 0; s < 64; s++)
+      if ((one << s) >= c) break;
+    unsigned __int128 m = ((one << 64) * ((one << s) - c)) / c + 1;
+    qd_magic = (uint64_t)m;
+    qd_shift = s - 1;
+  }
+
+  // Allocates value rows for buckets [b0, b1), HBM while the budget lasts,
+  // then pinned host memory (include/table.h:130-242).
+  void add_slices(uint64_t b0, uint64_t b1) {
+    const uint64_t bps = 1ull << slice_shift;
+    for (uint64_t b = b0; b < b1; b += bps) {
+      const uint64_t nbk = std::min(bps, b1 - b);
+      const uint64_t bytes = std::max<uint64_t>(nbk * B * row, 256);
+      Slice s{nullptr, nullptr, true};
+      if (remaining_hbm >= bytes) {
+        hip_check(hipMalloc(&s.dev_ptr, bytes), "hipMalloc(values)");
+        remaining_hbm -= bytes;
+      } else {
+        hip_check(hipHostMalloc(&s.host_ptr, bytes, hipHostMallocDefault),
+                  "hipHostMalloc(values)");
+        hip_check(hipHostGetDevicePointer((void**)&s.dev_ptr, s.host_ptr, 0),
+                  "hipHostGetDevicePointer");
+        s.hbm = false;
+        pure_hbm = false;
+      }
+      slices.push_back(s);
+    }
+    if (slices.size() > d_slices_cap) {
+      if (d_slices) hip_check(hipFree(d_slices), "hipFree");
+      d_slices_cap = std::max<size_t>(slices.size() * 2, 16);
+      hip_check(hipMalloc(&d_slices, d_slices_cap * sizeof(uint8_t*)), "hipMalloc(slices)");
+    }
+    std::vector<uint8_t*> ptrs;
+    for (auto& s : slices) ptrs.push_back(s.dev_ptr);
+    hip_check(hipMemcpy(d_slices, ptrs.data(), ptrs.size() * sizeof(uint8_t*),
+                        hipMemcpyHostToDevice),
+              "hipMemcpy(slices)");
+  }
+
+  void free_all() {
+    (void)hipFree(digests);
+    (void)hipFree(keys);
+    (void)hipFree(scores);
+    (void)hipFree(bsize);
+    for (auto& s : slices) {
+      if (s.hbm) (void)hipFree(s.dev_ptr);
+      else (void)hipHostFree(s.host_ptr);
+    }
+    slices.clear();
+    (void)hipFree(d_slices);
+    (void)hipFree(cnt);
+    (void)hipFree(pend);
+    (void)hipFree(heavy);
+    (void)hipFree(ctrl);
+    (void)hipFree(blk);
+    (void)hipFree(d_sum);
+    if (h_sum) (void)hipHostFree(h_sum);
+  }
+
+  uint64_t clock_now() const {
+    if (clock_override) return clock_value;
+    return (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(
+               std::chrono::steady_clock::now().time_since_epoch())
+        .count();
+  }
+
+  void ensure_route_scratch(uint64_t n, uint32_t P) {
+    const uint64_t need = nb * P;
+    if (need > pend_cap) {
+      if (pend) hip_check(hipFree(pend), "hipFree");
+      hip_check(hipMalloc(&pend, need * sizeof(uint32_t)), "hipMalloc(pend)");
+      pend_cap = need;
+    }
+    const uint64_t hneed = n / (P + 1) + 1;
+    if (hneed > heavy_cap) {
+      if (heavy) hip_check(hipFree(heavy), "hipFree");
+      hip_check(hipMalloc(&heavy, hneed * sizeof(uint32_t)), "hipMalloc(heavy)");
+      heavy_cap = hneed;
+    }
+  }
+
+  // Pending-list length: large enough that, with keys spread uniformly, a
+  // bucket overflows it with negligible probability.
+  uint32_t pick_P(uint64_t n) const {
+    const double lam = (double)n / (double)nb;
+    if (lam <= 3.0) return 16;
+    if (lam <= 10.0) return 32;
+    if (lam <= 20.0) return 48;
+    return 64;
+  }
+
+  uint64_t sampled_size(hipStream_t s) {
+    const uint64_t N = std::min<uint64_t>(nb, 1024);
+    launch_fill_u64(d_sum, 0, 1, s);
+    launch_size(view(), N, d_sum, s);
+    hip_check(hipMemcpyAsync(h_sum, d_sum, sizeof(uint64_t), hipMemcpyDeviceToHost, s),
+              "hipMemcpyAsync");
+    hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
+    return *h_sum;
+  }
+
+  // fast_load_factor (include/hkv_hashtable.h:3229-3268).
+  float fast_load_factor(uint64_t delta, hipStream_t s) {
+    const uint64_t N = std::min<uint64_t>(nb, 1024);
+    const uint64_t tot = sampled_size(s);
+    return (float)((delta * 1.0) / (C * 1.0) + (tot * 1.0) / (B * N * 1.0));
+  }
+
+  void double_capacity(hipStream_t s) {
+    // include/table.h:360-377 followed by the rehash kernel.
+    const uint64_t old_nb = nb, old_C = C;
+    uint8_t* nd = nullptr;
+    uint64_t *nk = nullptr, *ns = nullptr;
+    int32_t* nbs = nullptr;
+    uint32_t* ncnt = nullptr;
+    hip_check(hipMalloc(&nd, 2 * old_C), "hipMalloc(digests)");
+    hip_check(hipMalloc(&nk, 2 * old_C * 8), "hipMalloc(keys)");
+    hip_check(hipMalloc(&ns, 2 * old_C * 8), "hipMalloc(scores)");
+    hip_check(hipMalloc(&nbs, 2 * old_nb * 4), "hipMalloc(bsize)");
+    hip_check(hipMalloc(&ncnt, 2 * old_nb * 4), "hipMalloc(cnt)");
+    hip_check(hipMemcpyAsync(nd, digests, old_C, hipMemcpyDeviceToDevice, s), "copy");
+    hip_check(hipMemcpyAsync(nk, keys, old_C * 8, hipMemcpyDeviceToDevice, s), "copy");
+    hip_check(hipMemcpyAsync(ns, scores, old_C * 8, hipMemcpyDeviceToDevice, s), "copy");
+    hip_check(hipMemcpyAsync(nbs, bsize, old_nb * 4, hipMemcpyDeviceToDevice, s), "copy");
+    launch_fill_u32(ncnt, 0, 2 * old_nb, s);
+    hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
+    (void)hipFree(digests);
+    (void)hipFree(keys);
+    (void)hipFree(scores);
+    (void)hipFree(bsize);
+    (void)hipFree(cnt);
+    digests = nd;
+    keys = nk;
+    scores = ns;
+    bsize = nbs;
+    cnt = ncnt;
+    nb = 2 * old_nb;
+    set_capacity(2 * old_C);
+    add_slices(old_nb, nb);
+    launch_init_slots(view(), old_nb, nb, s);
+    launch_rehash(view(), old_nb, value_unit(nullptr), s);
+    hip_check(hipGetLastError(), "rehash launch");
+    hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
+  }
+
+  // include/hkv_hashtable.h:2873-2935
+  void reserve(uint64_t new_cap, hipStream_t s) {
+    if (reach_max || new_cap > opt.max_capacity) {
+      reach_max = (C * 2 > opt.max_capacity);
+      return;
+    }
+    hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    while (C < new_cap && C * 2 <= opt.max_capacity) double_capacity(s);
+    hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    reach_max = (C * 2 > opt.max_capacity);
+  }
+
+  void maybe_grow(uint64_t n, hipStream_t s) {
+    while (!reach_max && fast_load_factor(n, s) > opt.max_load_factor) reserve(C * 2, s);
+  }
+
+  // check_evict_strategy (include/hkv_hashtable.h:3270-3298), plus a check
+  // that strategies which read input scores receive them.
+  void check_scores(int st, const uint64_t* sc, bool ignore) const {
+    if (!ignore) {
+      if ((st == HKV_LRU || st == HKV_EPOCH_LRU) && sc)
+        fail(HKV_ERR_INVALID,
+             "the scores should not be specified when running on LRU or Epoch LRU mode.");
+      if ((st == HKV_LFU || st == HKV_EPOCH_LFU) && !sc)
+        fail(HKV_ERR_INVALID,
+             "the scores should be specified when running on LFU or Epoch LFU mode.");
+      if (st == HKV_CUSTOMIZED && !sc)
+        fail(HKV_ERR_INVALID,
+             "the scores should be specified when running on customized mode.");
+      if ((st == HKV_EPOCH_LRU || st == HKV_EPOCH_LFU) && epoch == kIgnoredEpoch)
+        fail(HKV_ERR_INVALID,
+             "the global_epoch is invalid and should be assigned by calling "
+             "`set_global_epoch` when running on Epoch LRU or Epoch LFU mode.");
+    } else if ((st == HKV_LFU || st == HKV_EPOCH_LFU || st == HKV_CUSTOMIZED) && !sc) {
+      fail(HKV_ERR_INVALID, "this evict strategy reads input scores; scores is null.");
+    }
+  }
+
+  // Largest copy unit dividing the row size and the alignment of `p`.
+  int value_unit(const void* p) const {
+    uint64_t a = (uint64_t)(uintptr_t)p | row;
+    if (p == nullptr) a = row;
+    for (int u = 16; u > 1; u >>= 1)
+      if ((a & (u - 1)) == 0) return u;
+    return 1;
+  }
+};
+
+namespace {
+
+template <class F>
+int guarded(F&& f) {
+  try {
+    f();
+    return HKV_OK;
+  } catch (const HkvError& e) {
+    g_last_error = e.msg;
+    return e.code;
+  } catch (const std::bad_alloc&) {
+    g_last_error = "host allocation failed";
+    return HKV_ERR_DEVICE;
+  } catch (...) {
+    g_last_error = "unknown error";
+    return HKV_ERR_DEVICE;
+  }
+}
+
+void need_table(const hkv_table* t) {
+  if (!t) fail(HKV_ERR_INVALID, "null table handle");
+}
+
+hipStream_t S(hkv_stream s) { return reinterpret_cast<hipStream_t>(s); }
+
+int min_unit(const hkv_table* t, std::initializer_list<const void*> ps) {
+  int u = 16;
+  for (const void* p : ps)
+    if (p) u = std::min(u, t->value_unit(p));
+  return std::min(u, t->value_unit(nullptr));
+}
+
+int insert_like(hkv_table* t, int op, uint64_t n, const void* keys, const void* in_values,
+                void* io_values, const uint64_t* scores, const uint8_t* accum,
+                void* ev_keys, void* ev_values, uint64_t* ev_scores, uint64_t* ev_counter,
+                int strategy, int rule, hipStream_t s) {
+  ApplyArgs a{};
+  a.keys = reinterpret_cast<const uint64_t*>(keys);
+  a.in_values = reinterpret_cast<const uint8_t*>(in_values);
+  a.io_values = reinterpret_cast<uint8_t*>(io_values);
+  a.in_scores = scores;
+  a.accum_flags = accum;
+  a.ev_keys = reinterpret_cast<uint64_t*>(ev_keys);
+  a.ev_values = reinterpret_cast<uint8_t*>(ev_values);
+  a.ev_scores = ev_scores;
+  a.ev_counter = ev_counter;
+  a.n = n;
+  a.sc.strategy = strategy;
+  a.sc.epoch = t->epoch;
+  a.sc.clock = t->clock_now();
+  a.rule = rule;
+  a.unit = min_unit(t, {in_values, io_values, ev_values});
+  a.value_type = t->value_type;
+  const uint32_t P = t->pick_P(n);
+  t->ensure_route_scratch(n, P);
+  RouteScratch rs{t->cnt, t->pend, t->heavy, t->ctrl, P};
+  launch_apply(t->view(), op, a, rs, t->parity, s);
+  t->parity ^= 1;
+  hip_check(hipGetLastError(), "kernel launch");
+  return HKV_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+void hkv_options_default(hkv_options* o) {
+  std::memset(o, 0, sizeof(*o));
+  o->max_bucket_size = 128;
+  o->dim = 64;
+  o->max_load_factor = 0.5f;
+  o->block_size = 128;
+  o->io_block_size = 1024;
+  o->device_id = -1;
+  o->num_of_buckets_per_alloc = 1;
+}
+
+int hkv_create(const hkv_options* o, int key_type, int value_type, int strategy,
+               hkv_table** out) {
+  return guarded([&] {
+    if (!o || !out) fail(HKV_ERR_INVALID, "null argument");
+    *out = nullptr;
+    if (key_type != HKV_KEY_U64 && key_type != HKV_KEY_I64)
+      fail(HKV_ERR_INVALID, "The key_type must be int64_t or uint64_t.");
+    if (value_size(value_type) == 0) fail(HKV_ERR_INVALID, "unknown value type");
+    if (strategy < HKV_LRU || strategy > HKV_CUSTOMIZED)
+      fail(HKV_ERR_INVALID, "unknown evict strategy");
+    // include/hkv_hashtable.h:991-1024
+    if (o->reserved_key_start_bit < 0 || o->reserved_key_start_bit > 62)
+      fail(HKV_ERR_INVALID, "options.reserved_key_start_bit should >= 0 and <= 62.");
+    if (o->max_bucket_size < 16)
+      fail(HKV_ERR_INVALID, "Bucket size should be greater than or equal to 16");
+    if (!ispow2(o->max_bucket_size)) fail(HKV_ERR_INVALID, "Bucket size should be the pow of 2");
+    if (!ispow2(o->num_of_buckets_per_alloc))
+      fail(HKV_ERR_INVALID, "Then `num_of_buckets_per_alloc` should be the pow of 2");
+    if (o->init_capacity < o->num_of_buckets_per_alloc * o->max_bucket_size)
+      fail(HKV_ERR_INVALID,
+           "Then `num_of_buckets_per_alloc` must be equal or less than initial required "
+           "buckets number");
+    if ((o->max_bucket_size * 16) % 128 != 0)
+      fail(HKV_ERR_INVALID,
+           "Storage size of keys and scores in one bucket should be the mutiple of cache "
+           "line size");
+    if (o->io_by_cpu && o->max_hbm_for_vectors != 0)
+      fail(HKV_ERR_INVALID,
+           "[HierarchicalKV] `io_by_cpu` should not be true when `max_hbm_for_vectors` is not 0!");
+    if (o->io_by_cpu) fail(HKV_ERR_UNSUPPORTED, "io_by_cpu is not supported by this build");
+    if (o->api_lock) fail(HKV_ERR_UNSUPPORTED, "api_lock is not supported by this build");
+    if (o->max_bucket_size != 128)
+      fail(HKV_ERR_UNSUPPORTED, "this build supports max_bucket_size == 128");
+    if (o->dim == 0) fail(HKV_ERR_INVALID, "dim must be positive");
+
+    auto* t = new hkv_table();
+    t->opt = *o;
+    t->key_type = key_type;
+    t->value_type = value_type;
+    t->strategy = strategy;
+    t->B = o->max_bucket_size;
+    t->row = o->dim * (uint64_t)value_size(value_type);
+    try {
+      if (o->device_id >= 0) {
+        hip_check(hipSetDevice(o->device_id), "hipSetDevice");
+        t->device = o->device_id;
+      } else {
+        hip_check(hipGetDevice(&t->device), "hipGetDevice");
+        t->opt.device_id = t->device;
+      }
+      const uint64_t maxc = std::max(o->init_capacity, o->max_capacity);
+      t->opt.max_capacity = maxc;
+      // create_table bucket count (include/table.h:299-311).
+      if (o->init_capacity * 2 > maxc) {
+        t->nb = 1 + (maxc - 1) / t->B;
+      } else {
+        t->nb = 1;
+        while (t->nb * t->B < o->init_capacity) t->nb *= 2;
+      }
+      t->set_capacity(t->nb * t->B);
+      t->reach_max = (o->init_capacity * 2 > maxc);
+      // Value slices: one slice for everything when it all fits in HBM,
+      // otherwise power-of-two bucket groups of about the reference's slice
+      // size.
+      t->remaining_hbm = o->max_hbm_for_vectors;
+      const uint64_t all_bytes = t->nb * t->B * t->row;
+      if (t->remaining_hbm >= all_bytes) {
+        t->slice_shift = log2_ceil(t->nb);
+      } else {
+        const uint64_t sb = ref_slice_bytes(maxc, t->B, t->row);
+        uint64_t bps = std::max<uint64_t>(1, sb / (t->B * t->row));
+        uint32_t sh = 0;
+        while ((2ull << sh) <= bps) sh++;
+        t->slice_shift = std::min<uint64_t>(sh, log2_ceil(t->nb));
+      }
+      hip_check(hipMalloc(&t->digests, t->C), "hipMalloc(digests)");
+      hip_check(hipMalloc(&t->keys, t->C * 8), "hipMalloc(keys)");
+      hip_check(hipMalloc(&t->scores, t->C * 8), "hipMalloc(scores)");
+      hip_check(hipMalloc(&t->bsize, t->nb * 4), "hipMalloc(bsize)");
+      hip_check(hipMalloc(&t->cnt, t->nb * 4), "hipMalloc(cnt)");
+      hip_check(hipMalloc(&t->ctrl, 32 * sizeof(uint32_t)), "hipMalloc(ctrl)");
+      hip_check(hipMalloc(&t->d_sum, sizeof(uint64_t)), "hipMalloc(sum)");
+      hip_check(hipHostMalloc(&t->h_sum, sizeof(uint64_t), hipHostMallocDefault),
+                "hipHostMalloc(sum)");
+      t->add_slices(0, t->nb);
+      launch_init_slots(t->view(), 0, t->nb, 0);
+      launch_fill_u32(t->cnt, 0, t->nb, 0);
+      launch_fill_u32(t->ctrl, 0, 32, 0);
+      hip_check(hipGetLastError(), "init launch");
+      hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    } catch (...) {
+      t->free_all();
+      delete t;
+      throw;
+    }
+    *out = t;
+  });
+}
+
+int hkv_destroy(hkv_table* t) {
+  return guarded([&] {
+    if (!t) return;
+    (void)hipDeviceSynchronize();
+    t->free_all();
+    delete t;
+  });
+}
+
+int hkv_insert_or_assign(hkv_table* t, uint64_t n, const void* keys, const void* values,
+                         const uint64_t* scores, hkv_stream stream, int unique_key,
+                         int ignore_evict_strategy) {
+  return guarded([&] {
+    need_table(t);
+    // include/hkv_hashtable.h:1077-1215: ignore_evict_strategy instantiates
+    // the kCustomized functor for this call.
+    const int st = ignore_evict_strategy ? HKV_CUSTOMIZED : t->strategy;
+    if (n == 0) return;
+    if (!keys || !values) fail(HKV_ERR_INVALID, "keys and values must not be null");
+    t->maybe_grow(n, S(stream));
+    t->check_scores(st, scores, ignore_evict_strategy != 0);
+    insert_like(t, OP_INSERT_OR_ASSIGN, n, keys, values, nullptr, scores, nullptr, nullptr,
+                nullptr, nullptr, nullptr, st, unique_key ? RULE_DIGEST16 : RULE_TILE32,
+                S(stream));
+  });
+}
+
+int hkv_insert_and_evict(hkv_table* t, uint64_t n, const void* keys, const void* values,
+                         const uint64_t* scores, void* evicted_keys, void* evicted_values,
+                         uint64_t* evicted_scores, uint64_t* d_evicted_counter,
+                         hkv_stream stream, int unique_key, int ignore_evict_strategy) {
+  return guarded([&] {
+    need_table(t);
+    // include/hkv_hashtable.h:1260-1324
+    if (n == 0) return;
+    if (!keys || !values || !evicted_keys || !evicted_values || !d_evicted_counter) return;
+    t->maybe_grow(n, S(stream));
+    t->check_scores(t->strategy, scores, ignore_evict_strategy != 0);
+    if (!t->pure_hbm) fail(HKV_ERR_RUNTIME, "Only allow insert_and_evict in pure HBM mode.");
+    insert_like(t, OP_INSERT_AND_EVICT, n, keys, values, nullptr, scores, nullptr,
+                evicted_keys, evicted_values, evicted_scores, d_evicted_counter, t->strategy,
+                unique_key ? RULE_DIGEST16 : RULE_TILE32, S(stream));
+  });
+}
+
+int hkv_accum_or_assign(hkv_table* t, uint64_t n, const void* keys, const void* vals,
+                        const uint8_t* accum, const uint64_t* scores, hkv_stream stream,
+                        int ignore_evict_strategy) {
+  return guarded([&] {
+    need_table(t);
+    // include/hkv_hashtable.h:1438-1507
+    if (t->value_type == HKV_F64 || t->value_type == HKV_U16 || t->value_type == HKV_U32)
+      fail(HKV_ERR_RUNTIME,
+           "[accum_or_assign] Does not support double/uint16_t/uint32_t value_type.");
+    if (!(t->value_type == HKV_F32 || t->value_type == HKV_I32 || t->value_type == HKV_I64 ||
+          t->value_type == HKV_U64))
+      fail(HKV_ERR_UNSUPPORTED, "accum_or_assign supports f32/i32/i64/u64 values in this build");
+    if (n == 0) return;
+    if (!keys || !vals || !accum) fail(HKV_ERR_INVALID, "null argument");
+    t->maybe_grow(n, S(stream));
+    t->check_scores(t->strategy, scores, ignore_evict_strategy != 0);
+    insert_like(t, OP_ACCUM_OR_ASSIGN, n, keys, vals, nullptr, scores, accum, nullptr, nullptr,
+                nullptr, nullptr, t->strategy, RULE_TILE32, S(stream));
+  });
+}
+
+int hkv_find_or_insert(hkv_table* t, uint64_t n, const void* keys, void* values,
+                       const uint64_t* scores, hkv_stream stream, int unique_key,
+                       int ignore_evict_strategy) {
+  return guarded([&] {
+    need_table(t);
+    // include/hkv_hashtable.h:1526-1632
+    if (n == 0) return;
+    if (!keys || !values) fail(HKV_ERR_INVALID, "keys and values must not be null");
+    t->maybe_grow(n, S(stream));
+    t->check_scores(t->strategy, scores, ignore_evict_strategy != 0);
+    insert_like(t, OP_FIND_OR_INSERT, n, keys, values, values, scores, nullptr, nullptr,
+                nullptr, nullptr, nullptr, t->strategy,
+                unique_key ? RULE_DIGEST16 : RULE_TILE32, S(stream));
+  });
+}
+
+int hkv_assign_scores(hkv_table* t, uint64_t n, const void* keys, const uint64_t* scores,
+                      hkv_stream stream, int unique_key) {
+  return guarded([&] {
+    need_table(t);
+    // include/hkv_hashtable.h:1943-1977
+    (void)unique_key;
+    if (n == 0) return;
+    t->check_scores(t->strategy, scores, false);
+    if (!keys) fail(HKV_ERR_INVALID, "keys must not be null");
+    insert_like(t, OP_ASSIGN_SCORES, n, keys, nullptr, nullptr, scores, nullptr, nullptr,
+                nullptr, nullptr, nullptr, t->strategy, RULE_DIGEST16, S(stream));
+  });
+}
+
+int hkv_find(hkv_table* t, uint64_t n, const void* keys, void* values, uint8_t* founds,
+             uint64_t* scores, hkv_stream stream) {
+  return guarded([&] {
+    need_table(t);
+    if (n == 0) return;
+    if (!keys || !values) fail(HKV_ERR_INVALID, "keys and values must not be null");
+    launch_find(t->view(), reinterpret_cast<const uint64_t*>(keys), n,
+                reinterpret_cast<uint8_t*>(values), founds, scores, t->value_unit(values),
+                S(stream));
+    hip_check(hipGetLastError(), "find launch");
+  });
+}
+
+int hkv_find_missed(hkv_table* t, uint64_t n, const void* keys, void* values,
+                    void* missed_keys, int32_t* missed_indices, int32_t* missed_size,
+                    uint64_t* scores, hkv_stream stream) {
+  return guarded([&] {
+    need_table(t);
+    if (n == 0) return;
+    if (!keys || !values || !missed_keys || !missed_indices || !missed_size)
+      fail(HKV_ERR_INVALID, "null argument");
+    launch_fill_u32(reinterpret_cast<uint32_t*>(missed_size), 0, 1, S(stream));
+    launch_find_missed(t->view(), reinterpret_cast<const uint64_t*>(keys), n,
+                       reinterpret_cast<uint8_t*>(values),
+                       reinterpret_cast<uint64_t*>(missed_keys), missed_indices, missed_size,
+                       scores, t->value_unit(values), S(stream));
+    hip_check(hipGetLastError(), "find launch");
+  });
+}
+
+int hkv_erase(hkv_table* t, uint64_t n, const void* keys, hkv_stream stream) {
+  return guarded([&] {
+    need_table(t);
+    if (n == 0) return;
+    if (!keys) fail(HKV_ERR_INVALID, "keys must not be null");
+    launch_erase(t->view(), reinterpret_cast<const uint64_t*>(keys), n, S(stream));
+    hip_check(hipGetLastError(), "erase launch");
+  });
+}
+
+int hkv_clear(hkv_table* t, hkv_stream stream) {
+  return guarded([&] {
+    need_table(t);
+    launch_clear(t->view(), S(stream));
+    hip_check(hipGetLastError(), "clear launch");
+  });
+}
+
+int hkv_export_batch(hkv_table* t, uint64_t n, uint64_t offset, uint64_t* d_counter,
+                     void* keys, void* values, uint64_t* scores, hkv_stream stream) {
+  return guarded([&] {
+    need_table(t);
+    if (!d_counter) fail(HKV_ERR_INVALID, "d_counter must not be null");
+    launch_fill_u64(d_counter, 0, 1, S(stream));
+    if (offset >= t->C) return;
+    n = std::min(t->C - offset, n);
+    if (n == 0) return;
+    if (!keys || !values) fail(HKV_ERR_INVALID, "keys and values must not be null");
+    const uint64_t nblk = (n + 255) / 256;
+    if (nblk > t->blk_cap) {
+      if (t->blk) hip_check(hipFree(t->blk), "hipFree");
+      hip_check(hipMalloc(&t->blk, nblk * sizeof(uint32_t)), "hipMalloc(export)");
+      t->blk_cap = nblk;
+    }
+    launch_export(t->view(), offset, n, d_counter, reinterpret_cast<uint64_t*>(keys),
+                  reinterpret_cast<uint8_t*>(values), scores, t->blk, t->value_unit(values),
+                  S(stream));
+    hip_check(hipGetLastError(), "export launch");
+  });
+}
+
+int hkv_reserve(hkv_table* t, uint64_t new_capacity, hkv_stream stream) {
+  return guarded([&] {
+    need_table(t);
+    t->reserve(new_capacity, S(stream));
+  });
+}
+
+int hkv_set_global_epoch(hkv_table* t, uint64_t epoch) {
+  return guarded([&] {
+    need_table(t);
+    t->epoch = epoch;
+  });
+}
+
+int hkv_size(hkv_table* t, hkv_stream stream, uint64_t* out) {
+  return guarded([&] {
+    need_table(t);
+    if (!out) fail(HKV_ERR_INVALID, "null output");
+    launch_fill_u64(t->d_sum, 0, 1, S(stream));
+    launch_size(t->view(), t->nb, t->d_sum, S(stream));
+    hip_check(hipMemcpyAsync(t->h_sum, t->d_sum, sizeof(uint64_t), hipMemcpyDeviceToHost,
+                             S(stream)),
+              "hipMemcpyAsync");
+    hip_check(hipStreamSynchronize(S(stream)), "hipStreamSynchronize");
+    *out = *t->h_sum;
+  });
+}
+
+int hkv_load_factor(hkv_table* t, hkv_stream stream, float* out) {
+  uint64_t sz = 0;
+  const int rc = hkv_size(t, stream, &sz);
+  if (rc == HKV_OK) *out = (float)((sz * 1.0) / (t->C * 1.0));
+  return rc;
+}
+
+uint64_t hkv_capacity(const hkv_table* t) { return t ? t->C : 0; }
+uint64_t hkv_dim(const hkv_table* t) { return t ? t->opt.dim : 0; }
+uint64_t hkv_max_bucket_size(const hkv_table* t) { return t ? t->B : 0; }
+uint64_t hkv_bucket_count(const hkv_table* t) { return t ? t->nb : 0; }
+int hkv_is_pure_hbm_mode(const hkv_table* t) { return t && t->pure_hbm ? 1 : 0; }
+const char* hkv_last_error(void) { return g_last_error.c_str(); }
+
+int hkv_set_lru_clock(hkv_table* t, uint64_t clock, int enable) {
+  return guarded([&] {
+    need_table(t);
+    t->clock_override = enable != 0;
+    t->clock_value = clock;
+  });
+}
+
+}  // extern "C"

@@ -1,0 +1,176 @@
+/*
+ * hkv_amd.h -- C ABI of the MI355X (gfx950) HierarchicalKV table.
+ *
+ * Every entry point takes plain pointers and sizes.  Batch buffers (keys,
+ * values, scores, founds, outputs) are device-accessible pointers: HBM, or
+ * host memory from hipHostMalloc.  All calls are asynchronous on `stream`
+ * unless noted, exactly like the reference's HashTable methods they replace.
+ *
+ * Return value: HKV_OK (0) or an error code; hkv_last_error() gives the
+ * message of the last failure on the calling thread.  The C++ facade
+ * (hkv_hashtable.hpp) rethrows these as HkvException / NpuException /
+ * std::runtime_error, matching the reference's error convention
+ * (include/debug.h:30-74).
+ *
+ * Reference interfaces replaced (paths relative to the reference root):
+ *   HashTableOptions            include/hashtable_options.h:33-65
+ *   HashTable::init             include/hkv_hashtable.h:962-1042
+ *   HashTable::insert_or_assign include/hkv_hashtable.h:1077-1215
+ *   HashTable::insert_and_evict include/hkv_hashtable.h:1260-1324, :1368-1396
+ *   HashTable::accum_or_assign  include/hkv_hashtable.h:1438-1507
+ *   HashTable::find_or_insert   include/hkv_hashtable.h:1526-1632
+ *   HashTable::assign_scores    include/hkv_hashtable.h:1943-1977
+ *   HashTable::find             include/hkv_hashtable.h:2113-2152
+ *   HashTable::find (missed)    include/hkv_hashtable.h:2175-2220
+ *   HashTable::erase            include/hkv_hashtable.h:2358-2376
+ *   HashTable::clear            include/hkv_hashtable.h:2482-2493
+ *   HashTable::export_batch     include/hkv_hashtable.h:2519-2577
+ *   HashTable::size             include/hkv_hashtable.h:2792-2819
+ *   HashTable::reserve          include/hkv_hashtable.h:2873-2935
+ *   HashTable::load_factor      include/hkv_hashtable.h:2945-2947
+ *   HashTable::set_global_epoch include/hkv_hashtable.h:3197
+ *   capacity/dim/max_bucket_size/bucket_count/is_pure_hbm_mode accessors
+ *                               include/hkv_hashtable.h:2849, :171-871
+ * The launch glue it also replaces: include/aclnn_helper.h (reductions),
+ * include/simt_vf_dispatcher.h (template dispatch), include/tiling_helper.h.
+ */
+#ifndef HKV_AMD_H_
+#define HKV_AMD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct hkv_table hkv_table;
+/* A hipStream_t; 0 is the null stream. */
+typedef void* hkv_stream;
+
+enum hkv_status {
+  HKV_OK = 0,
+  HKV_ERR_INVALID = 1,     /* argument/option check (HkvException)        */
+  HKV_ERR_RUNTIME = 2,     /* unsupported mode for this call (runtime_error) */
+  HKV_ERR_UNSUPPORTED = 3, /* not available in this build                 */
+  HKV_ERR_DEVICE = 4,      /* HIP runtime failure (NpuException)          */
+};
+
+/* Eviction strategies, include/hkv_hashtable.h:111-119. */
+enum hkv_strategy {
+  HKV_LRU = 0,
+  HKV_LFU = 1,
+  HKV_EPOCH_LRU = 2,
+  HKV_EPOCH_LFU = 3,
+  HKV_CUSTOMIZED = 4,
+};
+
+/* Key types (template parameter K). */
+enum hkv_key_type { HKV_KEY_U64 = 0, HKV_KEY_I64 = 1 };
+
+/* Value element types (template parameter V). */
+enum hkv_value_type {
+  HKV_F32 = 0, HKV_F64 = 1, HKV_F16 = 2, HKV_BF16 = 3,
+  HKV_I8 = 4, HKV_U8 = 5, HKV_I16 = 6, HKV_U16 = 7,
+  HKV_I32 = 8, HKV_U32 = 9, HKV_I64 = 10, HKV_U64 = 11,
+};
+
+/* Field-for-field HashTableOptions (include/hashtable_options.h:33-65);
+ * the memory-pool sub-options are not carried (the library allocates its
+ * scratch itself). */
+typedef struct hkv_options {
+  uint64_t init_capacity;
+  uint64_t max_capacity;
+  uint64_t max_hbm_for_vectors; /* bytes; values beyond it go to pinned host */
+  uint64_t max_bucket_size;     /* 128 */
+  uint64_t dim;                 /* 64 */
+  float max_load_factor;        /* 0.5 */
+  int32_t block_size;           /* accepted, not used */
+  int32_t io_block_size;        /* accepted, not used */
+  int32_t device_id;            /* -1: current device */
+  int32_t io_by_cpu;            /* must be 0 */
+  int32_t use_constant_memory;  /* reserved */
+  int32_t reserved_key_start_bit;
+  uint64_t num_of_buckets_per_alloc;
+  int32_t api_lock;             /* must be 0 */
+} hkv_options;
+
+/* Fills the reference's defaults. */
+void hkv_options_default(hkv_options* opt);
+
+/* HashTable<K,V,S=uint64_t,Strategy>::init.  Synchronous. */
+int hkv_create(const hkv_options* opt, int key_type, int value_type,
+               int strategy, hkv_table** out);
+int hkv_destroy(hkv_table* t);
+
+int hkv_insert_or_assign(hkv_table* t, uint64_t n, const void* keys,
+                         const void* values, const uint64_t* scores,
+                         hkv_stream stream, int unique_key,
+                         int ignore_evict_strategy);
+
+/* `d_evicted_counter` is accumulated into (not cleared), as in the
+ * reference; insert_and_evict throws in hybrid mode. */
+int hkv_insert_and_evict(hkv_table* t, uint64_t n, const void* keys,
+                         const void* values, const uint64_t* scores,
+                         void* evicted_keys, void* evicted_values,
+                         uint64_t* evicted_scores, uint64_t* d_evicted_counter,
+                         hkv_stream stream, int unique_key,
+                         int ignore_evict_strategy);
+
+int hkv_accum_or_assign(hkv_table* t, uint64_t n, const void* keys,
+                        const void* value_or_deltas,
+                        const uint8_t* accum_or_assigns,
+                        const uint64_t* scores, hkv_stream stream,
+                        int ignore_evict_strategy);
+
+int hkv_find_or_insert(hkv_table* t, uint64_t n, const void* keys,
+                       void* values, const uint64_t* scores, hkv_stream stream,
+                       int unique_key, int ignore_evict_strategy);
+
+int hkv_assign_scores(hkv_table* t, uint64_t n, const void* keys,
+                      const uint64_t* scores, hkv_stream stream,
+                      int unique_key);
+
+/* Missed rows of `values` are left untouched; `scores` may be NULL. */
+int hkv_find(hkv_table* t, uint64_t n, const void* keys, void* values,
+             uint8_t* founds, uint64_t* scores, hkv_stream stream);
+
+/* `missed_size` (device int) is cleared by the call. */
+int hkv_find_missed(hkv_table* t, uint64_t n, const void* keys, void* values,
+                    void* missed_keys, int32_t* missed_indices,
+                    int32_t* missed_size, uint64_t* scores, hkv_stream stream);
+
+int hkv_erase(hkv_table* t, uint64_t n, const void* keys, hkv_stream stream);
+int hkv_clear(hkv_table* t, hkv_stream stream);
+
+/* Exports live slots [offset, offset + n) in slot order; `d_counter`
+ * (device uint64) receives the count. */
+int hkv_export_batch(hkv_table* t, uint64_t n, uint64_t offset,
+                     uint64_t* d_counter, void* keys, void* values,
+                     uint64_t* scores, hkv_stream stream);
+
+/* Synchronous. */
+int hkv_reserve(hkv_table* t, uint64_t new_capacity, hkv_stream stream);
+int hkv_set_global_epoch(hkv_table* t, uint64_t epoch);
+
+/* Synchronous (stream is synchronized). */
+int hkv_size(hkv_table* t, hkv_stream stream, uint64_t* out);
+int hkv_load_factor(hkv_table* t, hkv_stream stream, float* out);
+
+uint64_t hkv_capacity(const hkv_table* t);
+uint64_t hkv_dim(const hkv_table* t);
+uint64_t hkv_max_bucket_size(const hkv_table* t);
+uint64_t hkv_bucket_count(const hkv_table* t);
+int hkv_is_pure_hbm_mode(const hkv_table* t);
+
+const char* hkv_last_error(void);
+
+/* Test hook with no reference counterpart: fixes the LRU clock used by
+ * Lru/EpochLru (the reference reads a device cycle counter per launch).
+ * enable=0 returns to the host monotonic clock read once per call. */
+int hkv_set_lru_clock(hkv_table* t, uint64_t clock, int enable);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* HKV_AMD_H_ */
