@@ -257,59 +257,59 @@ __global__ __launch_bounds__(kBlock) void k_route(TableView t, const uint64_t* _
 
 enum Outcome : uint32_t { R_DUP = 1, R_EMPTY = 2, R_RECLAIMED = 3, R_EVICT = 4, R_REFUSED = 5 };
 
-// State of one bucket held by a 16-lane group: lane l owns slots l + 16*j.
-template <int SPL>
+// State of one bucket held by a 16-lane group: lane l owns slots l + 16*j
+// (j = 0..7).  Only the owner lane ever reads or writes a slot's key, score
+// and digest, so the slots need no register cache: the owner re-reads them
+// (same-thread ordering makes its own earlier writes visible).  The eight
+// digests of a lane are kept packed in two words.
 struct Bucket16 {
   uint64_t b;
   uint64_t base;  // b * B
   uint32_t l;
-  uint32_t dg[SPL];
-  uint64_t kv[SPL];
-  uint64_t sv[SPL];
-  uint32_t kvalid, svalid;
+  uint32_t dg0, dg1;  // digest of slot l+16j in byte j (dg0: j<4, dg1: j>=4)
+  uint32_t live_ed;   // slots seen holding a live key with the empty digest
   int32_t bsz, bsz0;
 };
 
-template <int SPL>
-__device__ __forceinline__ void bucket_load(const TableView& t, Bucket16<SPL>& S, uint64_t b,
+__device__ __forceinline__ uint32_t dg_of(const Bucket16& S, uint32_t j) {
+  return ((j < 4 ? S.dg0 : S.dg1) >> (8 * (j & 3))) & 0xFFu;
+}
+
+__device__ __forceinline__ void dg_set(Bucket16& S, uint32_t j, uint32_t d) {
+  const uint32_t sh = 8 * (j & 3);
+  const uint32_t m = ~(0xFFu << sh);
+  if (j < 4) S.dg0 = (S.dg0 & m) | (d << sh);
+  else S.dg1 = (S.dg1 & m) | (d << sh);
+}
+
+__device__ __forceinline__ void bucket_load(const TableView& t, Bucket16& S, uint64_t b,
                                             uint32_t l) {
   S.b = b;
   S.base = b * (uint64_t)t.B;
   S.l = l;
-#pragma unroll
-  for (int j = 0; j < SPL; j++) S.dg[j] = t.digests[S.base + l + 16 * j];
-  S.kvalid = 0;
-  S.svalid = 0;
+  const uint8_t* dg = t.digests + S.base + l;
+  S.dg0 = (uint32_t)dg[0] | ((uint32_t)dg[16] << 8) | ((uint32_t)dg[32] << 16) |
+          ((uint32_t)dg[48] << 24);
+  S.dg1 = (uint32_t)dg[64] | ((uint32_t)dg[80] << 8) | ((uint32_t)dg[96] << 16) |
+          ((uint32_t)dg[112] << 24);
+  S.live_ed = 0;
   S.bsz = S.bsz0 = t.bsize[b];
 }
 
-template <int SPL>
-__device__ __forceinline__ uint64_t sel_u64(const uint64_t (&a)[SPL], uint32_t j) {
-  uint64_t r = 0;
-#pragma unroll
-  for (int q = 0; q < SPL; q++)
-    if ((uint32_t)q == j) r = a[q];
-  return r;
-}
-
-template <int SPL>
-__device__ __forceinline__ void set_u64(uint64_t (&a)[SPL], uint32_t j, uint64_t v) {
-#pragma unroll
-  for (int q = 0; q < SPL; q++)
-    if ((uint32_t)q == j) a[q] = v;
-}
-
-// Group-wide minimum of (score, rank) carrying the slot.
-__device__ __forceinline__ void group_min_score(uint64_t& s, uint32_t& rank, uint32_t& pos) {
+// Group-wide minimum of (score, rank) carrying the slot and its key.
+__device__ __forceinline__ void group_min_victim(uint64_t& s, uint32_t& rank, uint32_t& pos,
+                                                 uint64_t& key) {
 #pragma unroll
   for (int m = 8; m > 0; m >>= 1) {
     const uint64_t os = shfl_xor_u64(s, m, 16);
     const uint32_t orank = __shfl_xor(rank, m, 16);
     const uint32_t opos = __shfl_xor(pos, m, 16);
+    const uint64_t okey = shfl_xor_u64(key, m, 16);
     if (os < s || (os == s && orank < rank)) {
       s = os;
       rank = orank;
       pos = opos;
+      key = okey;
     }
   }
 }
@@ -341,8 +341,10 @@ __device__ __forceinline__ void accum_row(uint8_t* dst, const uint8_t* delta, ui
 // this with the same i).  Restates, for one key, the reference kernels
 // insert_or_assign_kernel.h:76-303 (unique keys) and find_and_lock
 // (find_utils.h:94-227) with its callers (non-unique keys and accum).
-template <int OP, int SPL>
-__device__ void apply_key(const TableView& t, Bucket16<SPL>& S, const ApplyArgs& a, uint64_t i) {
+template <int OP, int U>
+__device__ __forceinline__ void apply_key(const TableView& t, Bucket16& S, const ApplyArgs& a,
+                                          uint64_t i) {
+  constexpr int SPL = 8;
   const uint32_t B = t.B;
   const uint32_t l = S.l;
   const uint64_t k = a.keys[i];
@@ -353,21 +355,14 @@ __device__ void apply_key(const TableView& t, Bucket16<SPL>& S, const ApplyArgs&
   const uint32_t start = (uint32_t)(gi & (B - 1));
   const uint32_t d = (uint32_t)(h >> 32) & 0xFFu;
   const uint64_t des = score_desired(a.sc, has_in, in);
+  const uint64_t* kp = t.keys + S.base + l;
 
   // 1. Is the key present?  Candidates are digest matches.
-  uint32_t need = 0;
-#pragma unroll
-  for (int j = 0; j < SPL; j++)
-    if (S.dg[j] == d && !((S.kvalid >> j) & 1u)) need |= 1u << j;
-#pragma unroll
-  for (int j = 0; j < SPL; j++)
-    if ((need >> j) & 1u) S.kv[j] = t.keys[S.base + l + 16 * j];
-  S.kvalid |= need;
   const uint32_t a4 = start & ~3u;
   uint32_t best = kNone;
 #pragma unroll
   for (int j = 0; j < SPL; j++) {
-    if (S.dg[j] == d && S.kv[j] == k) {
+    if (dg_of(S, j) == d && kp[16 * j] == k) {
       const uint32_t p = l + 16 * j;
       const uint32_t rk = (((p - a4) & (B - 1)) << 8) | p;
       best = rk < best ? rk : best;
@@ -390,8 +385,7 @@ __device__ void apply_key(const TableView& t, Bucket16<SPL>& S, const ApplyArgs&
         uint32_t rl = kNone;
 #pragma unroll
         for (int j = 0; j < SPL; j++) {
-          const bool known_live = ((S.kvalid >> j) & 1u) && S.kv[j] != kEmptyKey;
-          if (S.dg[j] == kEmptyDigest && !known_live) {
+          if (dg_of(S, j) == kEmptyDigest && !((S.live_ed >> j) & 1u)) {
             const uint32_t r = (l + 16 * j - start) & (B - 1);
             rl = r < rl ? r : rl;
           }
@@ -399,17 +393,14 @@ __device__ void apply_key(const TableView& t, Bucket16<SPL>& S, const ApplyArgs&
         const uint32_t r = group_min_u32(rl);
         if (r == kNone) break;
         const uint32_t p = (start + r) & (B - 1);
-        const uint32_t owner = p & 15u, jj = p >> 4;
-        uint64_t kk = 0;
+        const uint32_t owner = p & 15u;
+        uint32_t is_empty = 0;
         if (l == owner) {
-          if (!((S.kvalid >> jj) & 1u)) {
-            set_u64<SPL>(S.kv, jj, t.keys[S.base + p]);
-            S.kvalid |= 1u << jj;
-          }
-          kk = sel_u64<SPL>(S.kv, jj);
+          is_empty = t.keys[S.base + p] == kEmptyKey;
+          if (!is_empty) S.live_ed |= 1u << (p >> 4);
         }
-        kk = shfl_u64(kk, (int)owner, 16);
-        if (kk == kEmptyKey) {
+        is_empty = __shfl(is_empty, (int)owner, 16);
+        if (is_empty) {
           res = R_EMPTY;
           pos = p;
           break;
@@ -417,22 +408,15 @@ __device__ void apply_key(const TableView& t, Bucket16<SPL>& S, const ApplyArgs&
       }
     }
     if (res == 0) {
-      // 3. Eviction: every key and score of the bucket is needed.
-      const uint32_t kneed = ~S.kvalid & ((1u << SPL) - 1);
-      const uint32_t sneed = ~S.svalid & ((1u << SPL) - 1);
-#pragma unroll
-      for (int j = 0; j < SPL; j++)
-        if ((kneed >> j) & 1u) S.kv[j] = t.keys[S.base + l + 16 * j];
-#pragma unroll
-      for (int j = 0; j < SPL; j++)
-        if ((sneed >> j) & 1u) S.sv[j] = t.scores[S.base + l + 16 * j];
-      S.kvalid = S.svalid = (1u << SPL) - 1;
-      uint64_t ms = kMaxScore;
+      // 3. Eviction over every slot of the bucket.
+      const uint64_t* sp = t.scores + S.base + l;
+      uint64_t ms = kMaxScore, mk = 0;
       uint32_t mr = kNone, mp = start;
 #pragma unroll
       for (int j = 0; j < SPL; j++) {
         const uint32_t p = l + 16 * j;
-        const uint64_t kj = S.kv[j];
+        const uint64_t kj = kp[16 * j];
+        const uint64_t sj = sp[16 * j];
         uint32_t rank;
         bool elig;
         if (a.rule == RULE_DIGEST16) {
@@ -445,25 +429,28 @@ __device__ void apply_key(const TableView& t, Bucket16<SPL>& S, const ApplyArgs&
           // find_and_lock: lane r%32 scans r, r+32, ...; lowest lane wins.
           elig = kj != kEmptyKey;
           const uint32_t r = (p - start) & (B - 1);
-          rank = B >= 32 ? (r & 31) * (B / 32) + (r >> 5) : r;
+          rank = (r & 31) * (B / 32) + (r >> 5);
         }
-        const uint64_t sj = S.sv[j];
         if (elig && sj < kMaxScore && (sj < ms || (sj == ms && rank < mr))) {
           ms = sj;
           mr = rank;
           mp = p;
+          mk = kj;
         }
       }
-      group_min_score(ms, mr, mp);
-      if (mr == kNone) mp = start;  // every eligible score is MAX_SCORE
+      group_min_victim(ms, mr, mp, mk);
+      if (mr == kNone) {
+        // Every eligible score is MAX_SCORE: the start slot is taken.
+        mp = start;
+        uint64_t kk = 0;
+        if (l == (start & 15u)) kk = t.keys[S.base + start];
+        mk = shfl_u64(kk, (int)(start & 15u), 16);
+      }
       if (des < ms) {
         res = R_REFUSED;
       } else {
         pos = mp;
-        const uint32_t owner = mp & 15u, jj = mp >> 4;
-        uint64_t kk = 0;
-        if (l == owner) kk = sel_u64<SPL>(S.kv, jj);
-        victim_key = shfl_u64(kk, (int)owner, 16);
+        victim_key = mk;
         victim_score = ms;
         res = victim_key == kReclaimKey ? R_RECLAIMED : R_EVICT;
       }
@@ -487,7 +474,7 @@ __device__ void apply_key(const TableView& t, Bucket16<SPL>& S, const ApplyArgs&
         a.ev_keys[j] = k;
         if (a.ev_scores) a.ev_scores[j] = des;
       }
-      copy_row(a.ev_values + j * R, in_row, R, a.unit, l, 16);
+      copy_units<U>(a.ev_values + j * R, in_row, R, l, 16);
     }
     return;
   }
@@ -500,33 +487,27 @@ __device__ void apply_key(const TableView& t, Bucket16<SPL>& S, const ApplyArgs&
       a.ev_keys[j] = victim_key;
       if (a.ev_scores) a.ev_scores[j] = victim_score;
     }
-    copy_row(a.ev_values + j * R, trow, R, a.unit, l, 16);
+    copy_units<U>(a.ev_values + j * R, trow, R, l, 16);
   }
   if (res == R_EMPTY || res == R_RECLAIMED) S.bsz++;
 
   if (res == R_DUP) {
     if (OP == OP_FIND_OR_INSERT) {
-      copy_row(a.io_values + i * (uint64_t)R, trow, R, a.unit, l, 16);
+      copy_units<U>(a.io_values + i * (uint64_t)R, trow, R, l, 16);
     } else if (OP == OP_ACCUM_OR_ASSIGN) {
       accum_row(trow, in_row, R, a.value_type, l, 16);
     } else if (OP != OP_ASSIGN_SCORES) {
-      copy_row(trow, in_row, R, a.unit, l, 16);
+      copy_units<U>(trow, in_row, R, l, 16);
     }
   } else {
-    copy_row(trow, in_row, R, a.unit, l, 16);
+    copy_units<U>(trow, in_row, R, l, 16);
   }
 
   const uint32_t owner = pos & 15u, jj = pos >> 4;
   if (l == owner) {
     uint64_t old = 0;
-    const bool need_old = a.sc.strategy == kLfu || a.sc.strategy == kEpochLfu;
-    if (res == R_DUP && need_old) {
-      if (!((S.svalid >> jj) & 1u)) {
-        set_u64<SPL>(S.sv, jj, t.scores[S.base + pos]);
-        S.svalid |= 1u << jj;
-      }
-      old = sel_u64<SPL>(S.sv, jj);
-    }
+    if (res == R_DUP && (a.sc.strategy == kLfu || a.sc.strategy == kEpochLfu))
+      old = t.scores[S.base + pos];
     bool w;
     uint64_t ns;
     if (OP == OP_ASSIGN_SCORES) {
@@ -538,38 +519,297 @@ __device__ void apply_key(const TableView& t, Bucket16<SPL>& S, const ApplyArgs&
     }
     if (w) {
       t.scores[S.base + pos] = ns;
-      set_u64<SPL>(S.sv, jj, ns);
-      S.svalid |= 1u << jj;
       if (res != R_DUP) {
         t.digests[S.base + pos] = (uint8_t)d;
-#pragma unroll
-        for (int q = 0; q < SPL; q++)
-          if ((uint32_t)q == jj) S.dg[q] = d;
+        dg_set(S, jj, d);
       }
     }
-    if (res != R_DUP) {
-      t.keys[S.base + pos] = k;
-      set_u64<SPL>(S.kv, jj, k);
-      S.kvalid |= 1u << jj;
+    if (res != R_DUP) t.keys[S.base + pos] = k;
+  }
+}
+
+__device__ __forceinline__ void bucket_finish(const TableView& t, Bucket16& S) {
+  if (S.l == 0 && S.bsz != S.bsz0) t.bsize[S.b] = S.bsz;
+}
+
+// Pending-count word after the lane-per-bucket pass: bits 0-15 hold the
+// number of routed keys, bit 31 marks a bucket handed to the 16-lane pass
+// and bits 16-30 the sorted position it resumes from.
+constexpr uint32_t kDefer = 0x80000000u;
+constexpr uint32_t kLightMax = 16;  // keys per bucket the lane pass holds
+
+// Row tasks queued by a wave of the lane pass, executed cooperatively.  The
+// destination pointer's top bit marks an accumulate task.
+constexpr uint32_t kTaskCap = 256;
+constexpr uint64_t kAccumBit = 1ull << 63;
+
+template <int U>
+__device__ __forceinline__ void flush_tasks(uint32_t ntask, const uint64_t* s_src,
+                                            const uint64_t* s_dst, uint32_t row_bytes,
+                                            int vt) {
+  using T = typename UnitT<U>::T;
+  constexpr int Q = 4;  // rows in flight per lane group
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t units = row_bytes / U;
+  uint32_t lpr = 64;
+  while (lpr > 1 && lpr / 2 >= units) lpr >>= 1;
+  const uint32_t rpi = 64 / lpr;
+  const uint32_t sub = lane % lpr;
+  // Rows beyond ntask read task 0's source (valid) and store nothing.
+  const uint64_t any_src = s_src[0] & ~kAccumBit;
+  for (uint32_t r0 = 0; r0 < ntask; r0 += Q * rpi) {
+    const T* s[Q];
+    T* d[Q];
+#pragma unroll
+    for (int q = 0; q < Q; q++) {
+      const uint32_t r = r0 + q * rpi + lane / lpr;
+      const bool ok = r < ntask;
+      uint64_t dp = ok ? s_dst[r] : 0;
+      const uint64_t sp = ok ? s_src[r] : any_src;
+      if (dp & kAccumBit) {
+        accum_row(reinterpret_cast<uint8_t*>((uintptr_t)(dp & ~kAccumBit)),
+                  reinterpret_cast<const uint8_t*>((uintptr_t)sp), row_bytes, vt, sub, lpr);
+        dp = 0;
+      }
+      s[q] = reinterpret_cast<const T*>((uintptr_t)(dp ? sp : any_src));
+      d[q] = reinterpret_cast<T*>((uintptr_t)dp);
+    }
+    for (uint32_t u = sub; u < units; u += lpr) {
+      T v0 = s[0][u], v1 = s[1][u], v2 = s[2][u], v3 = s[3][u];
+      if (d[0]) d[0][u] = v0;
+      if (d[1]) d[1][u] = v1;
+      if (d[2]) d[2][u] = v2;
+      if (d[3]) d[3][u] = v3;
     }
   }
 }
 
-template <int SPL>
-__device__ __forceinline__ void bucket_finish(const TableView& t, Bucket16<SPL>& S) {
-  if (S.l == 0 && S.bsz != S.bsz0) t.bsize[S.b] = S.bsz;
+// Digest probe of one key by one lane (insert_or_assign_kernel.h:105-183):
+// returns the slot holding `k` (dup=1), else the first EMPTY slot in circular
+// order from `start` when the bucket is not full (dup=0), else -1.
+__device__ __forceinline__ int probe_upsert(const TableView& t, uint64_t base, uint32_t start,
+                                            uint32_t d, uint64_t k, bool not_full, int* dup) {
+  const uint32_t B = t.B;
+  const uint8_t* dg = t.digests + base;
+  const uint64_t* ks = t.keys + base;
+  const uint32_t a = start & ~3u;
+  const uint32_t rep = d * 0x01010101u;
+  const uint32_t erep = (uint32_t)kEmptyDigest * 0x01010101u;
+  uint32_t cur = kNone;
+  uint4 chunk = make_uint4(0, 0, 0, 0);
+  for (uint32_t off = 0; off < B + 4; off += 4) {
+    const uint32_t g = (a + off) & (B - 1);
+    const uint32_t c = g >> 4;
+    if (c != cur) {
+      chunk = *reinterpret_cast<const uint4*>(dg + (c << 4));
+      cur = c;
+    }
+    const uint32_t wi = (g >> 2) & 3;
+    const uint32_t w = wi == 0 ? chunk.x : wi == 1 ? chunk.y : wi == 2 ? chunk.z : chunk.w;
+    uint32_t m = eq_bytes4(w, rep);
+    while (m) {
+      const uint32_t j = __builtin_ctz(m);
+      m &= m - 1;
+      if (ks[g + j] == k) {
+        *dup = 1;
+        return (int)(g + j);
+      }
+    }
+    if (!not_full) continue;
+    uint32_t e = eq_bytes4(w, erep);
+    while (e) {
+      const uint32_t j = __builtin_ctz(e);
+      e &= e - 1;
+      const uint32_t p = g + j;
+      if (off == 0 && p < start) continue;
+      if (ks[p] == kEmptyKey) {
+        *dup = 0;
+        return (int)p;
+      }
+    }
+  }
+  return -1;
 }
 
-// One 16-lane group per bucket with 1..P routed keys.
-template <int OP, int SPL>
+// Lane-per-bucket pass: each lane owns one bucket with 1..16 routed keys and
+// applies them in batch order as long as no eviction is needed (the key is
+// present, or an EMPTY slot exists).  At the first key that would evict or be
+// refused the lane stops and hands the rest of the bucket to the 16-lane
+// pass.  Metadata is updated in place by the owning lane; row movements are
+// queued in LDS and executed cooperatively by the wave: at the end for
+// insert_or_assign / insert_and_evict, after every step for operations that
+// read table rows (find_or_insert, accum_or_assign) so that a later key of
+// the same batch sees an earlier key's row.
+template <int OP, int U>
+__global__ __launch_bounds__(kBlock) void k_apply_lpb(TableView t, ApplyArgs a,
+                                                      uint32_t* __restrict__ cnt,
+                                                      const uint32_t* __restrict__ pend,
+                                                      uint32_t P) {
+  __shared__ uint64_t s_src[kBlock / 64][kTaskCap];
+  __shared__ uint64_t s_dst[kBlock / 64][kTaskCap];
+  constexpr bool kStepFlush = OP == OP_FIND_OR_INSERT || OP == OP_ACCUM_OR_ASSIGN;
+  const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const uint64_t b = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
+  const uint32_t B = t.B;
+  const uint32_t R = t.row_bytes;
+  uint32_t c = 0;
+  if (b < t.buckets) c = cnt[b];
+  const bool light = c > 0 && c <= P && c <= kLightMax;
+  uint32_t e[kLightMax];
+#pragma unroll
+  for (uint32_t q = 0; q < kLightMax; q++) e[q] = (light && q < c) ? pend[b * P + q] + 1u : 0u;
+  const uint64_t base = b * (uint64_t)B;
+  int32_t bsz = light ? t.bsize[b] : 0;
+  const int32_t bsz0 = bsz;
+  uint32_t maxc = light ? c : 0;
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) {
+    const uint32_t o = __shfl_xor(maxc, m, 64);
+    maxc = o > maxc ? o : maxc;
+  }
+  // Slots whose row is already queued for writing in this call; a second
+  // write to one of them flushes the queue first so that the later key wins.
+  uint32_t wr0 = 0, wr1 = 0, wr2 = 0, wr3 = 0;
+  bool active = light;
+  uint32_t stop = c;
+  uint32_t ntask = 0;
+  const bool has_in = a.in_scores != nullptr;
+  // One-step-ahead prefetch of the next key (batch order).
+  uint32_t m_next = kNone;
+#pragma unroll
+  for (uint32_t q = 0; q < kLightMax; q++)
+    if (e[q] > 0 && e[q] < m_next) m_next = e[q];
+  uint64_t k_next = 0, in_next = 0;
+  if (light) {
+    k_next = a.keys[m_next - 1];
+    if (has_in) in_next = a.in_scores[m_next - 1];
+  }
+  for (uint32_t step = 0; step < maxc; step++) {
+    uint64_t src = 0, dst = 0;
+    bool conflict = false;
+    if (active && step < c) {
+      const uint32_t m = m_next;
+      const uint64_t i = m - 1;
+      const uint64_t k = k_next;
+      const uint64_t in = in_next;
+      m_next = kNone;
+#pragma unroll
+      for (uint32_t q = 0; q < kLightMax; q++)
+        if (e[q] > m && e[q] < m_next) m_next = e[q];
+      if (m_next != kNone) {
+        k_next = a.keys[m_next - 1];
+        if (has_in) in_next = a.in_scores[m_next - 1];
+      }
+      const uint64_t h = murmur3(k);
+      const uint64_t gi = global_idx(t, h);
+      const uint32_t start = (uint32_t)(gi & (B - 1));
+      const uint32_t d = (uint32_t)(h >> 32) & 0xFFu;
+      int dup = 0;
+      const bool may_insert = OP != OP_ASSIGN_SCORES;
+      const int p = probe_upsert(t, base, start, d, k, may_insert && bsz < (int32_t)B, &dup);
+      if (p < 0 && may_insert) {
+        active = false;  // eviction path: hand over from this key on
+        stop = step;
+      } else if (p >= 0) {
+        const uint64_t des = score_desired(a.sc, has_in, in);
+        bool apply = true;
+        if (OP == OP_ACCUM_OR_ASSIGN) {
+          const bool is_accum = a.accum_flags[i] != 0;
+          apply = is_accum == (dup != 0);
+        }
+        if (apply) {
+          uint8_t* trow = row_ptr(t, b, (uint32_t)p);
+          const uint8_t* in_row = a.in_values ? a.in_values + i * (uint64_t)R : nullptr;
+          bool w;
+          if (dup) {
+            uint64_t old = 0;
+            if (a.sc.strategy == kLfu || a.sc.strategy == kEpochLfu) old = t.scores[base + p];
+            const uint64_t ns = OP == OP_ASSIGN_SCORES
+                                    ? score_wo_missed(a.sc, has_in, in, old, &w)
+                                    : score_hit(a.sc, has_in, in, des, old, &w);
+            if (w) t.scores[base + p] = ns;
+            if (OP == OP_FIND_OR_INSERT) {
+              src = (uint64_t)(uintptr_t)trow;
+              dst = (uint64_t)(uintptr_t)(a.io_values + i * (uint64_t)R);
+            } else if (OP == OP_ACCUM_OR_ASSIGN) {
+              src = (uint64_t)(uintptr_t)in_row;
+              dst = (uint64_t)(uintptr_t)trow | kAccumBit;
+            } else if (OP != OP_ASSIGN_SCORES) {
+              src = (uint64_t)(uintptr_t)in_row;
+              dst = (uint64_t)(uintptr_t)trow;
+            }
+          } else {
+            const uint64_t ns = score_new(a.sc, has_in, in, des, t.scores[base + p], &w);
+            if (w) {
+              t.scores[base + p] = ns;
+              t.digests[base + p] = (uint8_t)d;
+            }
+            t.keys[base + p] = k;
+            bsz++;
+            src = (uint64_t)(uintptr_t)in_row;
+            dst = (uint64_t)(uintptr_t)trow;
+          }
+          if (!kStepFlush && dst) {
+            const uint32_t bit = 1u << (p & 31);
+            const uint32_t wq = (uint32_t)p >> 5;
+            const uint32_t cur = wq == 0 ? wr0 : wq == 1 ? wr1 : wq == 2 ? wr2 : wr3;
+            conflict = (cur & bit) != 0;
+            wr0 |= wq == 0 ? bit : 0u;
+            wr1 |= wq == 1 ? bit : 0u;
+            wr2 |= wq == 2 ? bit : 0u;
+            wr3 |= wq == 3 ? bit : 0u;
+          }
+        }
+      }
+    }
+    // Queue this step's row tasks; flush first when full or when a slot is
+    // written twice.
+    const uint64_t tm = __ballot(dst != 0);
+    const uint32_t nnew = __popcll(tm);
+    if (kStepFlush || __ballot(conflict) != 0 || ntask + nnew > kTaskCap) {
+      __builtin_amdgcn_wave_barrier();
+      if (ntask) flush_tasks<U>(ntask, s_src[wv], s_dst[wv], R, a.value_type);
+      ntask = 0;
+      if (kStepFlush) __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+      __builtin_amdgcn_wave_barrier();
+    }
+    if (dst) {
+      const uint32_t r = ntask + __popcll(tm & ((1ull << lane) - 1));
+      s_src[wv][r] = src;
+      s_dst[wv][r] = dst;
+    }
+    ntask += nnew;
+    if (kStepFlush) {
+      __builtin_amdgcn_wave_barrier();
+      if (ntask) flush_tasks<U>(ntask, s_src[wv], s_dst[wv], R, a.value_type);
+      ntask = 0;
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+      __builtin_amdgcn_wave_barrier();
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  if (ntask) flush_tasks<U>(ntask, s_src[wv], s_dst[wv], R, a.value_type);
+  if (light) {
+    if (bsz != bsz0) t.bsize[b] = bsz;
+    cnt[b] = stop == c ? 0u : (kDefer | (stop << 16) | c);
+  }
+}
+
+// One 16-lane group per bucket the lane pass did not finish: buckets with
+// more than 16 (and at most P) routed keys, and buckets handed over at their
+// first eviction.
+template <int OP, int U>
 __global__ __launch_bounds__(kBlock) void k_apply(TableView t, ApplyArgs a,
                                                   uint32_t* __restrict__ cnt,
                                                   const uint32_t* __restrict__ pend, uint32_t P) {
   const uint64_t gid = ((uint64_t)blockIdx.x * kBlock + threadIdx.x) >> 4;
   const uint32_t l = threadIdx.x & 15;
   if (gid >= t.buckets) return;
-  const uint32_t c = cnt[gid];
-  if (c == 0 || c > P) return;
+  const uint32_t raw = cnt[gid];
+  if (raw == 0) return;
+  const uint32_t c = raw & 0xFFFFu;
+  if (c > P) return;
+  const uint32_t first = (raw & kDefer) ? (raw >> 16) & 0x7FFFu : 0u;
   // Pending indices of this bucket, up to 4 per lane, stored as index + 1.
   uint32_t e[4];
 #pragma unroll
@@ -577,8 +817,8 @@ __global__ __launch_bounds__(kBlock) void k_apply(TableView t, ApplyArgs a,
     const uint32_t s = l + 16 * q;
     e[q] = s < c ? pend[gid * P + s] + 1u : 0u;
   }
-  Bucket16<SPL> S;
-  bucket_load<SPL>(t, S, gid, l);
+  Bucket16 S;
+  bucket_load(t, S, gid, l);
   uint32_t last = 0;
   for (uint32_t step = 0; step < c; step++) {
     uint32_t m = kNone;
@@ -587,15 +827,15 @@ __global__ __launch_bounds__(kBlock) void k_apply(TableView t, ApplyArgs a,
       if (e[q] > last && e[q] < m) m = e[q];
     m = group_min_u32(m);
     last = m;
-    apply_key<OP, SPL>(t, S, a, (uint64_t)(m - 1));
+    if (step >= first) apply_key<OP, U>(t, S, a, (uint64_t)(m - 1));
   }
-  bucket_finish<SPL>(t, S);
+  bucket_finish(t, S);
   if (l == 0) cnt[gid] = 0;
 }
 
 // Buckets with more than P routed keys: one group per bucket walks the batch
 // in index order.
-template <int OP, int SPL>
+template <int OP, int U>
 __global__ __launch_bounds__(kBlock) void k_apply_heavy(TableView t, ApplyArgs a,
                                                         uint32_t* __restrict__ cnt,
                                                         const uint32_t* __restrict__ heavy,
@@ -607,8 +847,8 @@ __global__ __launch_bounds__(kBlock) void k_apply_heavy(TableView t, ApplyArgs a
   for (uint64_t g = ((uint64_t)blockIdx.x * kBlock + threadIdx.x) >> 4; g < nheavy;
        g += groups) {
     const uint64_t b = heavy[g];
-    Bucket16<SPL> S;
-    bucket_load<SPL>(t, S, b, l);
+    Bucket16 S;
+    bucket_load(t, S, b, l);
     for (uint64_t base = 0; base < a.n; base += 16) {
       const uint64_t i = base + l;
       bool mine = false;
@@ -620,10 +860,10 @@ __global__ __launch_bounds__(kBlock) void k_apply_heavy(TableView t, ApplyArgs a
       while (mask) {
         const uint32_t q = __builtin_ctz(mask);
         mask &= mask - 1;
-        apply_key<OP, SPL>(t, S, a, base + q);
+        apply_key<OP, U>(t, S, a, base + q);
       }
     }
-    bucket_finish<SPL>(t, S);
+    bucket_finish(t, S);
     if (l == 0) cnt[b] = 0;
   }
 }
@@ -913,13 +1153,24 @@ static void apply_op(const TableView& t, const ApplyArgs& a, RouteScratch& rs, i
   uint32_t* ctrl_next = rs.ctrl + 16 * (1 - parity);
   hipLaunchKernelGGL(k_route, dim3(grid_for(a.n, kBlock, 1ull << 31)), dim3(kBlock), 0, s, t,
                      a.keys, a.n, rs.cnt, rs.pend, rs.P, rs.heavy, ctrl, ctrl_next);
-  hipLaunchKernelGGL((k_apply<OP, 8>), dim3(grid_for(t.buckets * 16, kBlock, 1ull << 31)),
-                     dim3(kBlock), 0, s, t, a, rs.cnt, rs.pend, rs.P);
-  if (a.n > rs.P) {
-    const uint64_t max_heavy = a.n / (rs.P + 1) + 1;
-    hipLaunchKernelGGL((k_apply_heavy<OP, 8>), dim3(grid_for(max_heavy * 16, kBlock, 2048)),
-                       dim3(kBlock), 0, s, t, a, rs.cnt, rs.heavy, ctrl);
+  const dim3 gl(grid_for(t.buckets, kBlock, 1ull << 31)), bl(kBlock);
+  const dim3 gg(grid_for(t.buckets * 16, kBlock, 1ull << 31));
+  const uint64_t max_heavy = a.n / (rs.P + 1) + 1;
+  const dim3 gh(grid_for(max_heavy * 16, kBlock, 2048));
+  const bool heavy = a.n > rs.P;
+#define HKV_APPLY_U(UU)                                                                  \
+  hipLaunchKernelGGL((k_apply_lpb<OP, UU>), gl, bl, 0, s, t, a, rs.cnt, rs.pend, rs.P);  \
+  hipLaunchKernelGGL((k_apply<OP, UU>), gg, bl, 0, s, t, a, rs.cnt, rs.pend, rs.P);      \
+  if (heavy)                                                                             \
+    hipLaunchKernelGGL((k_apply_heavy<OP, UU>), gh, bl, 0, s, t, a, rs.cnt, rs.heavy, ctrl);
+  switch (a.unit) {
+    case 16: HKV_APPLY_U(16); break;
+    case 8: HKV_APPLY_U(8); break;
+    case 4: HKV_APPLY_U(4); break;
+    case 2: HKV_APPLY_U(2); break;
+    default: HKV_APPLY_U(1); break;
   }
+#undef HKV_APPLY_U
 }
 
 void launch_apply(const TableView& t, int op, const ApplyArgs& a, RouteScratch& rs, int parity,
