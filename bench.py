@@ -102,6 +102,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the load factor 0.75/1.0 and miss points")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="first run a plain 1 GiB device-to-device copy (the "
+                         "reference kernel for scaling HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: the table is a single-device "
@@ -114,6 +117,13 @@ def main():
 
     K, W = args.steps, args.warmup
     dev = torch.device("cuda:0")
+    if args.calibrate:
+        a = torch.empty(1 << 28, dtype=torch.float32, device=dev).fill_(1.0)
+        b_ = torch.empty_like(a)
+        torch.cuda.synchronize()
+        b_.copy_(a)
+        torch.cuda.synchronize()
+        del a, b_
     stream = torch.cuda.Stream(device=dev)
     gen = torch.Generator(device="cuda")
     gen.manual_seed(1234)
