@@ -1,0 +1,263 @@
+// hkv_hashtable.hpp -- header-only C++ facade of the gfx950 table with the
+// reference's API: npu::hkv::HashTable<K, V, S, Strategy> (reference
+// include/hkv_hashtable.h:895-3485), HashTableOptions
+// (include/hashtable_options.h:33-65), EvictStrategy (:111-119) and the
+// exception types of include/debug.h:30-74.  Every method forwards to the C
+// ABI in hkv_amd.h; link with libhkv_amd.so.  `aclrtStream` is a HIP stream.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+#include <type_traits>
+
+#include "hkv_amd.h"
+
+namespace npu {
+namespace hkv {
+
+using aclrtStream = hipStream_t;
+
+struct EvictStrategy {
+  enum EvictStrategyEnum {
+    kLru = HKV_LRU,
+    kLfu = HKV_LFU,
+    kEpochLru = HKV_EPOCH_LRU,
+    kEpochLfu = HKV_EPOCH_LFU,
+    kCustomized = HKV_CUSTOMIZED,
+  };
+};
+
+struct HashTableOptions {
+  size_t init_capacity = 0;
+  size_t max_capacity = 0;
+  size_t max_hbm_for_vectors = 0;
+  size_t max_bucket_size = 128;
+  size_t dim = 64;
+  float max_load_factor = 0.5f;
+  int block_size = 128;
+  int io_block_size = 1024;
+  int device_id = -1;
+  bool io_by_cpu = false;
+  bool use_constant_memory = false;
+  int reserved_key_start_bit = 0;
+  size_t num_of_buckets_per_alloc = 1;
+  bool api_lock = false;
+};
+
+class NpuException : public std::runtime_error {
+ public:
+  explicit NpuException(const std::string& what) : std::runtime_error(what) {}
+};
+
+class HkvException : public std::runtime_error {
+ public:
+  explicit HkvException(const std::string& what) : std::runtime_error(what) {}
+};
+
+namespace detail {
+
+inline void check(int rc) {
+  if (rc == HKV_OK) return;
+  const std::string msg = hkv_last_error();
+  switch (rc) {
+    case HKV_ERR_INVALID: throw HkvException(msg);
+    case HKV_ERR_RUNTIME: throw std::runtime_error(msg);
+    case HKV_ERR_UNSUPPORTED: throw std::invalid_argument(msg);
+    default: throw NpuException(msg);
+  }
+}
+
+template <class V> struct value_code;
+template <> struct value_code<float> { static constexpr int v = HKV_F32; };
+template <> struct value_code<double> { static constexpr int v = HKV_F64; };
+template <> struct value_code<int8_t> { static constexpr int v = HKV_I8; };
+template <> struct value_code<uint8_t> { static constexpr int v = HKV_U8; };
+template <> struct value_code<int16_t> { static constexpr int v = HKV_I16; };
+template <> struct value_code<uint16_t> { static constexpr int v = HKV_U16; };
+template <> struct value_code<int32_t> { static constexpr int v = HKV_I32; };
+template <> struct value_code<uint32_t> { static constexpr int v = HKV_U32; };
+template <> struct value_code<int64_t> { static constexpr int v = HKV_I64; };
+template <> struct value_code<uint64_t> { static constexpr int v = HKV_U64; };
+
+}  // namespace detail
+
+template <typename K, typename V, typename S = uint64_t,
+          int Strategy = EvictStrategy::kLru>
+class HashTable {
+ public:
+  using size_type = size_t;
+  using key_type = K;
+  using value_type = V;
+  using score_type = S;
+  static constexpr int evict_strategy = Strategy;
+
+  HashTable() {
+    static_assert(std::is_same<K, int64_t>::value || std::is_same<K, uint64_t>::value,
+                  "The key_type must be int64_t or uint64_t.");
+    static_assert(std::is_same<S, uint64_t>::value, "The score_type must be uint64_t.");
+  }
+  ~HashTable() {
+    if (t_) hkv_destroy(t_);
+    if (d_count_) (void)hipFree(d_count_);
+  }
+  HashTable(const HashTable&) = delete;
+  HashTable& operator=(const HashTable&) = delete;
+
+  void init(const HashTableOptions& o) {
+    if (t_) return;
+    hkv_options c;
+    hkv_options_default(&c);
+    c.init_capacity = o.init_capacity;
+    c.max_capacity = o.max_capacity;
+    c.max_hbm_for_vectors = o.max_hbm_for_vectors;
+    c.max_bucket_size = o.max_bucket_size;
+    c.dim = o.dim;
+    c.max_load_factor = o.max_load_factor;
+    c.block_size = o.block_size;
+    c.io_block_size = o.io_block_size;
+    c.device_id = o.device_id;
+    c.io_by_cpu = o.io_by_cpu;
+    c.use_constant_memory = o.use_constant_memory;
+    c.reserved_key_start_bit = o.reserved_key_start_bit;
+    c.num_of_buckets_per_alloc = o.num_of_buckets_per_alloc;
+    c.api_lock = o.api_lock;
+    detail::check(hkv_create(&c, std::is_same<K, int64_t>::value ? HKV_KEY_I64 : HKV_KEY_U64,
+                             detail::value_code<V>::v, Strategy, &t_));
+  }
+
+  void insert_or_assign(size_type n, const key_type* keys, const value_type* values,
+                        const score_type* scores = nullptr, aclrtStream stream = 0,
+                        bool unique_key = true, bool ignore_evict_strategy = false) {
+    detail::check(hkv_insert_or_assign(t_, n, keys, values, scores, stream, unique_key,
+                                       ignore_evict_strategy));
+  }
+
+  void insert_and_evict(size_type n, const key_type* keys, const value_type* values,
+                        const score_type* scores, key_type* evicted_keys,
+                        value_type* evicted_values, score_type* evicted_scores,
+                        size_type* d_evicted_counter, aclrtStream stream = 0,
+                        bool unique_key = true, bool ignore_evict_strategy = false) {
+    detail::check(hkv_insert_and_evict(t_, n, keys, values, scores, evicted_keys,
+                                       evicted_values, evicted_scores,
+                                       reinterpret_cast<uint64_t*>(d_evicted_counter), stream,
+                                       unique_key, ignore_evict_strategy));
+  }
+
+  size_type insert_and_evict(size_type n, const key_type* keys, const value_type* values,
+                             const score_type* scores, key_type* evicted_keys,
+                             value_type* evicted_values, score_type* evicted_scores,
+                             aclrtStream stream = 0, bool unique_key = true,
+                             bool ignore_evict_strategy = false) {
+    if (n == 0) return 0;
+    size_type* d = counter();
+    zero_counter(d, stream);
+    insert_and_evict(n, keys, values, scores, evicted_keys, evicted_values, evicted_scores, d,
+                     stream, unique_key, ignore_evict_strategy);
+    return read_counter(d, stream);
+  }
+
+  void accum_or_assign(size_type n, const key_type* keys, const value_type* value_or_deltas,
+                       const bool* accum_or_assigns, const score_type* scores = nullptr,
+                       aclrtStream stream = 0, bool ignore_evict_strategy = false) {
+    detail::check(hkv_accum_or_assign(t_, n, keys, value_or_deltas,
+                                      reinterpret_cast<const uint8_t*>(accum_or_assigns),
+                                      scores, stream, ignore_evict_strategy));
+  }
+
+  void find_or_insert(size_type n, const key_type* keys, value_type* values,
+                      score_type* scores = nullptr, aclrtStream stream = 0,
+                      bool unique_key = true, bool ignore_evict_strategy = false) {
+    detail::check(hkv_find_or_insert(t_, n, keys, values, scores, stream, unique_key,
+                                     ignore_evict_strategy));
+  }
+
+  void assign_scores(size_type n, const key_type* keys, const score_type* scores = nullptr,
+                     aclrtStream stream = 0, bool unique_key = true) {
+    detail::check(hkv_assign_scores(t_, n, keys, scores, stream, unique_key));
+  }
+
+  void find(size_type n, const key_type* keys, value_type* values, bool* founds,
+            score_type* scores = nullptr, aclrtStream stream = 0) const {
+    detail::check(hkv_find(t_, n, keys, values, reinterpret_cast<uint8_t*>(founds), scores,
+                           stream));
+  }
+
+  void find(size_type n, const key_type* keys, value_type* values, key_type* missed_keys,
+            int* missed_indices, int* missed_size, score_type* scores = nullptr,
+            aclrtStream stream = 0) const {
+    detail::check(hkv_find_missed(t_, n, keys, values, missed_keys, missed_indices,
+                                  missed_size, scores, stream));
+  }
+
+  void erase(size_type n, const key_type* keys, aclrtStream stream = 0) {
+    detail::check(hkv_erase(t_, n, keys, stream));
+  }
+
+  void clear(aclrtStream stream = 0) { detail::check(hkv_clear(t_, stream)); }
+
+  void export_batch(size_type n, size_type offset, size_type* d_counter, key_type* keys,
+                    value_type* values, score_type* scores = nullptr,
+                    aclrtStream stream = 0) const {
+    detail::check(hkv_export_batch(t_, n, offset, reinterpret_cast<uint64_t*>(d_counter),
+                                   keys, values, scores, stream));
+  }
+
+  size_type export_batch(size_type n, size_type offset, key_type* keys, value_type* values,
+                         score_type* scores = nullptr, aclrtStream stream = 0) const {
+    size_type* d = const_cast<HashTable*>(this)->counter();
+    export_batch(n, offset, d, keys, values, scores, stream);
+    return read_counter(d, stream);
+  }
+
+  void reserve(size_type new_capacity, aclrtStream stream = 0) {
+    detail::check(hkv_reserve(t_, new_capacity, stream));
+  }
+
+  void set_global_epoch(uint64_t epoch) { detail::check(hkv_set_global_epoch(t_, epoch)); }
+
+  size_type size(aclrtStream stream = 0) const {
+    uint64_t s = 0;
+    detail::check(hkv_size(t_, stream, &s));
+    return s;
+  }
+  float load_factor(aclrtStream stream = 0) const {
+    float f = 0;
+    detail::check(hkv_load_factor(t_, stream, &f));
+    return f;
+  }
+  size_type capacity() const { return hkv_capacity(t_); }
+  size_type dim() const noexcept { return hkv_dim(t_); }
+  size_type max_bucket_size() const noexcept { return hkv_max_bucket_size(t_); }
+  size_type bucket_count() const noexcept { return hkv_bucket_count(t_); }
+  bool is_pure_hbm_mode() const { return hkv_is_pure_hbm_mode(t_) != 0; }
+
+ private:
+  size_type* counter() {
+    if (!d_count_) {
+      if (hipMalloc(&d_count_, sizeof(size_type)) != hipSuccess)
+        throw NpuException("hipMalloc of the counter failed");
+    }
+    return d_count_;
+  }
+  static void zero_counter(size_type* d, aclrtStream stream) {
+    if (hipMemsetAsync(d, 0, sizeof(size_type), stream) != hipSuccess)
+      throw NpuException("hipMemsetAsync failed");
+  }
+  static size_type read_counter(size_type* d, aclrtStream stream) {
+    size_type h = 0;
+    if (hipMemcpyAsync(&h, d, sizeof(size_type), hipMemcpyDeviceToHost, stream) != hipSuccess ||
+        hipStreamSynchronize(stream) != hipSuccess)
+      throw NpuException("counter read failed");
+    return h;
+  }
+
+  hkv_table* t_ = nullptr;
+  size_type* d_count_ = nullptr;
+};
+
+}  // namespace hkv
+}  // namespace npu

@@ -1,0 +1,124 @@
+// C++ drop-in check: drives the gfx950 table through the header-only facade
+// (npu::hkv::HashTable, include/hkv_hashtable.hpp) exactly as reference code
+// would, and compares every result with the oracle (oracle/hkv_oracle.h).
+#include <hip/hip_runtime_api.h>
+
+#include <cstdio>
+#include <cstring>
+#include <random>
+#include <vector>
+
+#include "hkv_hashtable.hpp"
+#include "../../oracle/hkv_oracle.h"
+
+#define REQUIRE(c)                                                  \
+  do {                                                              \
+    if (!(c)) {                                                     \
+      std::printf("FAILED %s at line %d\n", #c, __LINE__);          \
+      return 1;                                                     \
+    }                                                               \
+  } while (0)
+
+template <class T>
+T* dev(const std::vector<T>& h) {
+  T* d = nullptr;
+  if (hipMalloc(&d, h.size() * sizeof(T) + 16) != hipSuccess) return nullptr;
+  hipMemcpy(d, h.data(), h.size() * sizeof(T), hipMemcpyHostToDevice);
+  return d;
+}
+
+template <class T>
+std::vector<T> host(const T* d, size_t n) {
+  std::vector<T> h(n);
+  hipMemcpy(h.data(), d, n * sizeof(T), hipMemcpyDeviceToHost);
+  return h;
+}
+
+int main() {
+  using namespace npu::hkv;
+  using Table = HashTable<uint64_t, float, uint64_t, EvictStrategy::kCustomized>;
+  const size_t cap = 1 << 14, dim = 8, n = 12000;
+  HashTableOptions opt;
+  opt.init_capacity = cap;
+  opt.max_capacity = cap;
+  opt.max_hbm_for_vectors = 1ull << 30;
+  opt.dim = dim;
+  Table table;
+  table.init(opt);
+  REQUIRE(table.capacity() == cap);
+  REQUIRE(table.dim() == dim);
+  REQUIRE(table.is_pure_hbm_mode());
+  int st = 0;
+  hkvo_table* o = hkvo_create(cap, cap, 128, dim, HKVO_F32, 4, 0.5f, &st);
+  REQUIRE(st == 0);
+
+  std::mt19937_64 rng(42);
+  std::vector<uint64_t> keys(n), scores(n);
+  std::vector<float> vals(n * dim);
+  for (size_t i = 0; i < n; i++) {
+    keys[i] = rng() >> 1;
+    scores[i] = rng() % 1000;
+    for (size_t j = 0; j < dim; j++) vals[i * dim + j] = (float)(rng() % 100000) * 1e-5f;
+  }
+  uint64_t* dk = dev(keys);
+  uint64_t* ds = dev(scores);
+  float* dv = dev(vals);
+  table.insert_or_assign(n, dk, dv, ds);
+  REQUIRE(hkvo_insert_or_assign(o, n, keys.data(), vals.data(), scores.data(), 1, 0, 0) == 0);
+  REQUIRE(table.size() == hkvo_size(o));
+
+  // find: founds, rows and scores bit-exact
+  std::vector<float> zero(n * dim, 0.f);
+  float* dout = dev(zero);
+  bool* dfound = nullptr;
+  uint64_t* dsc = nullptr;
+  hipMalloc(&dfound, n);
+  hipMalloc(&dsc, n * 8);
+  table.find(n, dk, dout, dfound, dsc);
+  hipDeviceSynchronize();
+  std::vector<float> ov(n * dim, 0.f);
+  std::vector<uint8_t> of(n);
+  std::vector<uint64_t> os(n);
+  hkvo_find(o, n, keys.data(), ov.data(), of.data(), os.data());
+  auto gv = host(dout, n * dim);
+  auto gf = host(reinterpret_cast<uint8_t*>(dfound), n);
+  auto gs = host(dsc, n);
+  REQUIRE(std::memcmp(gv.data(), ov.data(), n * dim * 4) == 0);
+  REQUIRE(std::memcmp(gf.data(), of.data(), n) == 0);
+  for (size_t i = 0; i < n; i++)
+    if (of[i]) REQUIRE(gs[i] == os[i]);
+
+  // erase a third, then export everything (slot order) and compare
+  table.erase(n / 3, dk);
+  hkvo_erase(o, n / 3, keys.data());
+  REQUIRE(table.size() == hkvo_size(o));
+  uint64_t* ek = nullptr;
+  float* ev = nullptr;
+  uint64_t* es = nullptr;
+  hipMalloc(&ek, cap * 8);
+  hipMalloc(&ev, cap * dim * 4);
+  hipMalloc(&es, cap * 8);
+  const size_t c = table.export_batch(cap, 0, ek, ev, es);
+  std::vector<uint64_t> xk(cap), xs(cap);
+  std::vector<float> xv(cap * dim);
+  const uint64_t oc = hkvo_export_batch(o, cap, 0, xk.data(), xv.data(), xs.data());
+  REQUIRE(c == oc);
+  auto hk = host(ek, c);
+  auto hv = host(ev, c * dim);
+  auto hs = host(es, c);
+  REQUIRE(std::memcmp(hk.data(), xk.data(), c * 8) == 0);
+  REQUIRE(std::memcmp(hs.data(), xs.data(), c * 8) == 0);
+  REQUIRE(std::memcmp(hv.data(), xv.data(), c * dim * 4) == 0);
+
+  // argument check surfaces as HkvException
+  bool threw = false;
+  try {
+    table.insert_or_assign(n, dk, dv, nullptr);
+  } catch (const HkvException&) {
+    threw = true;
+  }
+  REQUIRE(threw);
+  hkvo_destroy(o);
+  std::printf("facade parity ok: %zu keys, %zu exported\n", (size_t)table.size(), c);
+  return 0;
+}

@@ -85,3 +85,11 @@ def test_unknown_types_rejected():
     assert lib.hkv_create(ctypes.byref(o), 0, 99, 0, ctypes.byref(h)) == 1
     assert lib.hkv_create(ctypes.byref(o), 0, 0, 9, ctypes.byref(h)) == 1
     assert b"strategy" in lib.hkv_last_error()
+
+
+def test_cpp_facade_builds_and_links():
+    """The header-only npu::hkv::HashTable facade compiles against the C ABI
+    and links with libhkv_amd.so (run on a GPU by test_gpu_cpp_facade)."""
+    import subprocess
+    subprocess.check_call(["bash", os.path.join(ROOT, "tests", "cpp", "build.sh")])
+    assert os.path.exists(os.path.join(ROOT, "tests", "cpp", "build", "facade_parity"))
