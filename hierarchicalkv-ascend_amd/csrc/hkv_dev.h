@@ -44,6 +44,15 @@ __host__ __device__ __forceinline__ uint64_t murmur3(uint64_t k) {
   return k;
 }
 
+// Stored digest of a live key: byte 4 of its hash, except that the value of
+// the empty digest moves to the next value.  A slot whose digest equals
+// kEmptyDigest therefore holds EMPTY, and probes end or claim a slot on the
+// digest alone.  Lookups use the same mapping, so results are unchanged.
+__host__ __device__ __forceinline__ uint32_t key_digest(uint64_t h) {
+  const uint32_t d = (uint32_t)(h >> 32) & 0xFFu;
+  return d == kEmptyDigest ? kEmptyDigest + 1u : d;
+}
+
 struct TableView {
   uint8_t* digests;
   uint64_t* keys;

@@ -85,7 +85,7 @@ __device__ __forceinline__ int probe_find(const TableView& t, uint64_t b,
       e &= e - 1;
       const uint32_t p = g + j;
       if (off == 0 && p < start) continue;
-      if (ks[p] == kEmptyKey) return -1;
+      return -1;  // the empty digest marks an EMPTY slot
     }
   }
   return -1;
@@ -160,7 +160,7 @@ __global__ __launch_bounds__(kBlock) void k_find(TableView t, const uint64_t* __
       const uint64_t gi = global_idx(t, h);
       const uint64_t b = gi >> t.bshift;
       const uint32_t start = (uint32_t)(gi & (t.B - 1));
-      const int p = probe_find(t, b, start, (uint32_t)(h >> 32) & 0xFFu, k);
+      const int p = probe_find(t, b, start, key_digest(h), k);
       if (p >= 0) {
         found = true;
         src = row_ptr(t, b, (uint32_t)p);
@@ -208,7 +208,7 @@ __global__ __launch_bounds__(kBlock) void k_erase(TableView t, const uint64_t* _
   const uint64_t gi = global_idx(t, h);
   const uint64_t b = gi >> t.bshift;
   const uint32_t start = (uint32_t)(gi & (B - 1));
-  const uint32_t rep = ((uint32_t)(h >> 32) & 0xFFu) * 0x01010101u;
+  const uint32_t rep = key_digest(h) * 0x01010101u;
   uint8_t* dg = t.digests + b * B;
   uint64_t* ks = t.keys + b * B;
   const uint32_t a = start & ~3u;
@@ -267,7 +267,6 @@ struct Bucket16 {
   uint64_t base;  // b * B
   uint32_t l;
   uint32_t dg0, dg1;  // digest of slot l+16j in byte j (dg0: j<4, dg1: j>=4)
-  uint32_t live_ed;   // slots seen holding a live key with the empty digest
   int32_t bsz, bsz0;
 };
 
@@ -292,7 +291,6 @@ __device__ __forceinline__ void bucket_load(const TableView& t, Bucket16& S, uin
           ((uint32_t)dg[48] << 24);
   S.dg1 = (uint32_t)dg[64] | ((uint32_t)dg[80] << 8) | ((uint32_t)dg[96] << 16) |
           ((uint32_t)dg[112] << 24);
-  S.live_ed = 0;
   S.bsz = S.bsz0 = t.bsize[b];
 }
 
@@ -353,7 +351,7 @@ __device__ __forceinline__ void apply_key(const TableView& t, Bucket16& S, const
   const uint64_t h = murmur3(k);
   const uint64_t gi = global_idx(t, h);
   const uint32_t start = (uint32_t)(gi & (B - 1));
-  const uint32_t d = (uint32_t)(h >> 32) & 0xFFu;
+  const uint32_t d = key_digest(h);
   const uint64_t des = score_desired(a.sc, has_in, in);
   const uint64_t* kp = t.keys + S.base + l;
 
@@ -379,32 +377,20 @@ __device__ __forceinline__ void apply_key(const TableView& t, Bucket16& S, const
   } else if (OP == OP_ASSIGN_SCORES) {
     return;  // absent keys are a no-op
   } else {
-    // 2. First EMPTY slot in circular order from `start`.
+    // 2. First EMPTY slot (empty digest) in circular order from `start`.
     if (S.bsz < (int32_t)B) {
-      while (true) {
-        uint32_t rl = kNone;
+      uint32_t rl = kNone;
 #pragma unroll
-        for (int j = 0; j < SPL; j++) {
-          if (dg_of(S, j) == kEmptyDigest && !((S.live_ed >> j) & 1u)) {
-            const uint32_t r = (l + 16 * j - start) & (B - 1);
-            rl = r < rl ? r : rl;
-          }
+      for (int j = 0; j < SPL; j++) {
+        if (dg_of(S, j) == kEmptyDigest) {
+          const uint32_t r = (l + 16 * j - start) & (B - 1);
+          rl = r < rl ? r : rl;
         }
-        const uint32_t r = group_min_u32(rl);
-        if (r == kNone) break;
-        const uint32_t p = (start + r) & (B - 1);
-        const uint32_t owner = p & 15u;
-        uint32_t is_empty = 0;
-        if (l == owner) {
-          is_empty = t.keys[S.base + p] == kEmptyKey;
-          if (!is_empty) S.live_ed |= 1u << (p >> 4);
-        }
-        is_empty = __shfl(is_empty, (int)owner, 16);
-        if (is_empty) {
-          res = R_EMPTY;
-          pos = p;
-          break;
-        }
+      }
+      const uint32_t r = group_min_u32(rl);
+      if (r != kNone) {
+        res = R_EMPTY;
+        pos = (start + r) & (B - 1);
       }
     }
     if (res == 0) {
@@ -543,12 +529,11 @@ constexpr uint32_t kLightMax = 16;  // keys per bucket the lane pass holds
 constexpr uint32_t kTaskCap = 256;
 constexpr uint64_t kAccumBit = 1ull << 63;
 
-template <int U>
+template <int U, int Q>
 __device__ __forceinline__ void flush_tasks(uint32_t ntask, const uint64_t* s_src,
                                             const uint64_t* s_dst, uint32_t row_bytes,
                                             int vt) {
-  using T = typename UnitT<U>::T;
-  constexpr int Q = 4;  // rows in flight per lane group
+  using T = typename UnitT<U>::T;  // Q rows in flight per lane group: 2, 4 or 8
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t units = row_bytes / U;
   uint32_t lpr = 64;
@@ -575,11 +560,28 @@ __device__ __forceinline__ void flush_tasks(uint32_t ntask, const uint64_t* s_sr
       d[q] = reinterpret_cast<T*>((uintptr_t)dp);
     }
     for (uint32_t u = sub; u < units; u += lpr) {
-      T v0 = s[0][u], v1 = s[1][u], v2 = s[2][u], v3 = s[3][u];
-      if (d[0]) d[0][u] = v0;
-      if (d[1]) d[1][u] = v1;
-      if (d[2]) d[2][u] = v2;
-      if (d[3]) d[3][u] = v3;
+      if constexpr (Q == 2) {
+        const T v0 = s[0][u], v1 = s[1][u];
+        if (d[0]) d[0][u] = v0;
+        if (d[1]) d[1][u] = v1;
+      } else if constexpr (Q == 4) {
+        const T v0 = s[0][u], v1 = s[1][u], v2 = s[2][u], v3 = s[3][u];
+        if (d[0]) d[0][u] = v0;
+        if (d[1]) d[1][u] = v1;
+        if (d[2]) d[2][u] = v2;
+        if (d[3]) d[3][u] = v3;
+      } else {
+        const T v0 = s[0][u], v1 = s[1][u], v2 = s[2][u], v3 = s[3][u];
+        const T v4 = s[4][u], v5 = s[5][u], v6 = s[6][u], v7 = s[7][u];
+        if (d[0]) d[0][u] = v0;
+        if (d[1]) d[1][u] = v1;
+        if (d[2]) d[2][u] = v2;
+        if (d[3]) d[3][u] = v3;
+        if (d[4]) d[4][u] = v4;
+        if (d[5]) d[5][u] = v5;
+        if (d[6]) d[6][u] = v6;
+        if (d[7]) d[7][u] = v7;
+      }
     }
   }
 }
@@ -622,10 +624,8 @@ __device__ __forceinline__ int probe_upsert(const TableView& t, uint64_t base, u
       e &= e - 1;
       const uint32_t p = g + j;
       if (off == 0 && p < start) continue;
-      if (ks[p] == kEmptyKey) {
-        *dup = 0;
-        return (int)p;
-      }
+      *dup = 0;  // the empty digest marks an EMPTY slot
+      return (int)p;
     }
   }
   return -1;
@@ -703,7 +703,7 @@ __global__ __launch_bounds__(kBlock) void k_apply_lpb(TableView t, ApplyArgs a,
       const uint64_t h = murmur3(k);
       const uint64_t gi = global_idx(t, h);
       const uint32_t start = (uint32_t)(gi & (B - 1));
-      const uint32_t d = (uint32_t)(h >> 32) & 0xFFu;
+      const uint32_t d = key_digest(h);
       int dup = 0;
       const bool may_insert = OP != OP_ASSIGN_SCORES;
       const int p = probe_upsert(t, base, start, d, k, may_insert && bsz < (int32_t)B, &dup);
@@ -768,7 +768,7 @@ __global__ __launch_bounds__(kBlock) void k_apply_lpb(TableView t, ApplyArgs a,
     const uint32_t nnew = __popcll(tm);
     if (kStepFlush || __ballot(conflict) != 0 || ntask + nnew > kTaskCap) {
       __builtin_amdgcn_wave_barrier();
-      if (ntask) flush_tasks<U>(ntask, s_src[wv], s_dst[wv], R, a.value_type);
+      if (ntask) flush_tasks<U, 2>(ntask, s_src[wv], s_dst[wv], R, a.value_type);
       ntask = 0;
       if (kStepFlush) __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
       __builtin_amdgcn_wave_barrier();
@@ -781,14 +781,14 @@ __global__ __launch_bounds__(kBlock) void k_apply_lpb(TableView t, ApplyArgs a,
     ntask += nnew;
     if (kStepFlush) {
       __builtin_amdgcn_wave_barrier();
-      if (ntask) flush_tasks<U>(ntask, s_src[wv], s_dst[wv], R, a.value_type);
+      if (ntask) flush_tasks<U, 2>(ntask, s_src[wv], s_dst[wv], R, a.value_type);
       ntask = 0;
       __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
       __builtin_amdgcn_wave_barrier();
     }
   }
   __builtin_amdgcn_wave_barrier();
-  if (ntask) flush_tasks<U>(ntask, s_src[wv], s_dst[wv], R, a.value_type);
+  if (ntask) flush_tasks<U, 8>(ntask, s_src[wv], s_dst[wv], R, a.value_type);
   if (light) {
     if (bsz != bsz0) t.bsize[b] = bsz;
     cnt[b] = stop == c ? 0u : (kDefer | (stop << 16) | c);
@@ -1026,7 +1026,7 @@ __device__ void rehash_defrag(const TableView& t, uint64_t b, uint32_t remove_po
         (remove_pos < cur && cur < sp)) {
       t.keys[base + remove_pos] = ck;
       t.scores[base + remove_pos] = t.scores[base + cur];
-      t.digests[base + remove_pos] = (uint8_t)(h >> 32);
+      t.digests[base + remove_pos] = (uint8_t)key_digest(h);
       thread_copy(row_ptr(t, b, remove_pos), row_ptr(t, b, cur), t.row_bytes, unit);
       t.keys[base + cur] = kEmptyKey;
       t.digests[base + cur] = kEmptyDigest;
@@ -1069,7 +1069,7 @@ __global__ __launch_bounds__(kBlock) void k_rehash(TableView t, uint64_t old_nb,
       if (t.keys[nbase + cp] == kEmptyKey) {
         t.keys[nbase + cp] = ck;
         t.scores[nbase + cp] = cs;
-        t.digests[nbase + cp] = (uint8_t)(h >> 32);
+        t.digests[nbase + cp] = (uint8_t)key_digest(h);
         t.bsize[nbk]++;
         thread_copy(row_ptr(t, nbk, cp), row_ptr(t, b, kp), t.row_bytes, unit);
         break;
