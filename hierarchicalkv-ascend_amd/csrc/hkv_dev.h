@@ -1,10 +1,11 @@
 // hkv_dev.h -- device-side building blocks of the gfx950 HierarchicalKV table.
 //
 // Table layout in HBM (one table):
-//   digests  uint8 [buckets][B]   1-byte fingerprints, B = 128 slots/bucket
-//   keys     uint64[buckets][B]
-//   scores   uint64[buckets][B]
-//   bsize    int32 [buckets]      live keys per bucket
+//   digests  uint8 [buckets][B]     1-byte fingerprints, B = 128 slots/bucket
+//   slots    uint64[buckets][B][2]  16-byte slot records {key, score}: a slot's
+//                                   key and score share one 32-byte sector
+//   bsize    int32 [buckets]        live keys per bucket
+//   live     uint64                 live keys in the table (sum of bsize)
 //   values   rows of dim*sizeof(V) bytes, one per slot, in value slices:
 //            slice = slices[b >> slice_shift], row offset inside the slice =
 //            ((b & slice_mask) * B + slot) * row_bytes.  Slices live in HBM
@@ -53,11 +54,31 @@ __host__ __device__ __forceinline__ uint32_t key_digest(uint64_t h) {
   return d == kEmptyDigest ? kEmptyDigest + 1u : d;
 }
 
+// Pointers of the global address space.  Kernels reach table and batch
+// memory through pointers held in structs or passed between lanes, which the
+// compiler would otherwise treat as generic (flat) addresses: flat accesses
+// also count against the LDS wait counter and are slower to issue.  Casting
+// a generic pointer to global costs nothing on this target.
+template <class T>
+using gptr = __attribute__((address_space(1))) T*;
+template <class T>
+__device__ __forceinline__ gptr<T> G(T* p) {
+  return (gptr<T>)p;
+}
+template <class T>
+__device__ __forceinline__ gptr<T> G(uintptr_t p) {
+  return (gptr<T>)p;
+}
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint64_t u64x2 __attribute__((ext_vector_type(2)));
+using g64 = __attribute__((address_space(1))) uint64_t;
+
 struct TableView {
   uint8_t* digests;
-  uint64_t* keys;
-  uint64_t* scores;
+  uint64_t* slots;  // record of slot s at slots[2s] (key), slots[2s+1] (score)
   int32_t* bsize;
+  unsigned long long* live;
   uint8_t* const* slices;
   uint64_t capacity;
   uint64_t buckets;
@@ -70,6 +91,27 @@ struct TableView {
   uint32_t pow2;       // capacity is a power of two
 };
 
+__device__ __forceinline__ g64& slot_key(const TableView& t, uint64_t s) {
+  return G(t.slots)[2 * s];
+}
+__device__ __forceinline__ g64& slot_score(const TableView& t, uint64_t s) {
+  return G(t.slots)[2 * s + 1];
+}
+// Key (.x) and score (.y) of slot s in one 16-byte load.
+__device__ __forceinline__ u64x2 slot_load(const TableView& t, uint64_t s) {
+  return G(reinterpret_cast<u64x2*>(t.slots))[s];
+}
+__device__ __forceinline__ void slot_store(const TableView& t, uint64_t s, uint64_t k,
+                                           uint64_t sc) {
+  u64x2 v;
+  v.x = k;
+  v.y = sc;
+  G(reinterpret_cast<u64x2*>(t.slots))[s] = v;
+}
+__device__ __forceinline__ gptr<uint8_t> digest_row(const TableView& t, uint64_t b) {
+  return G(t.digests) + b * t.B;
+}
+
 // h mod capacity, exactly (reference include/utils.h:86-97 and the divisor
 // precomputation in include/table.h:106-127).
 __device__ __forceinline__ uint64_t global_idx(const TableView& t, uint64_t h) {
@@ -79,10 +121,10 @@ __device__ __forceinline__ uint64_t global_idx(const TableView& t, uint64_t h) {
   return h - (q >> t.qd_shift) * t.capacity;
 }
 
-__device__ __forceinline__ uint8_t* row_ptr(const TableView& t, uint64_t b,
-                                            uint32_t slot) {
+__device__ __forceinline__ gptr<uint8_t> row_ptr(const TableView& t, uint64_t b,
+                                                 uint32_t slot) {
   const uint64_t mask = (1ull << t.slice_shift) - 1;
-  uint8_t* base = t.slices[b >> t.slice_shift];
+  gptr<uint8_t> base = G(G(t.slices)[b >> t.slice_shift]);
   return base + ((b & mask) * t.B + slot) * (uint64_t)t.row_bytes;
 }
 
@@ -206,8 +248,8 @@ __device__ __forceinline__ uint32_t bitrev4(uint32_t x) {
 
 template <int U>
 struct UnitT;
-template <> struct UnitT<16> { using T = uint4; };
-template <> struct UnitT<8> { using T = uint2; };
+template <> struct UnitT<16> { using T = u32x4; };
+template <> struct UnitT<8> { using T = u32x2; };
 template <> struct UnitT<4> { using T = uint32_t; };
 template <> struct UnitT<2> { using T = uint16_t; };
 template <> struct UnitT<1> { using T = uint8_t; };
@@ -215,14 +257,12 @@ template <> struct UnitT<1> { using T = uint8_t; };
 // `nl` lanes (rank `r` among them) copy `bytes` from src to dst in U-byte
 // units.
 template <int U>
-__device__ __forceinline__ void copy_units(uint8_t* __restrict__ dst,
-                                           const uint8_t* __restrict__ src,
-                                           uint32_t bytes, uint32_t r,
-                                           uint32_t nl) {
+__device__ __forceinline__ void copy_units(gptr<uint8_t> dst, gptr<const uint8_t> src,
+                                           uint32_t bytes, uint32_t r, uint32_t nl) {
   using T = typename UnitT<U>::T;
   const uint32_t units = bytes / U;
-  T* d = reinterpret_cast<T*>(dst);
-  const T* s = reinterpret_cast<const T*>(src);
+  gptr<T> d = (gptr<T>)dst;
+  gptr<const T> s = (gptr<const T>)src;
   uint32_t u = r;
   for (; u + 3 * nl < units; u += 4 * nl) {
     const T a = s[u], b = s[u + nl], c = s[u + 2 * nl], e = s[u + 3 * nl];
@@ -234,7 +274,7 @@ __device__ __forceinline__ void copy_units(uint8_t* __restrict__ dst,
   for (; u < units; u += nl) d[u] = s[u];
 }
 
-__device__ __forceinline__ void copy_row(uint8_t* dst, const uint8_t* src,
+__device__ __forceinline__ void copy_row(gptr<uint8_t> dst, gptr<const uint8_t> src,
                                          uint32_t bytes, int unit, uint32_t r,
                                          uint32_t nl) {
   switch (unit) {

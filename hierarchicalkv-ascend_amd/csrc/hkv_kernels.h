@@ -46,6 +46,30 @@ struct RouteScratch {
   uint32_t P;
 };
 
+// Per-call scratch of the partitioned apply pipeline (owned by the table).
+// A partition is a run of 256 consecutive buckets; the batch is cut into
+// chunks of 1024 keys.  Segment (g, p) = the keys of chunk g that fall in
+// partition p.
+struct PartScratch {
+  uint32_t* hist;       // [chunks][partitions]: segment sizes, then offsets
+  uint64_t* ent;        // {key, batch index} entries: [partitions * cap + n][2]
+  uint32_t* pinfo;      // [partitions][2]: first entry, entry count
+  uint32_t* spill_top;  // entries placed past the fixed regions
+  uint64_t* trow;       // [n] row task per batch index, zero between calls
+  uint32_t* pflag;      // [partitions] 1 = applied by the single-run kernel
+  uint32_t* drec;       // [n][4] buckets handed to the 16-lane kernel
+  uint64_t* dpool;      // [n][2] their keys, {key, batch index}
+  uint32_t* dctr;       // [2] records, pool entries (zeroed by the count kernel)
+  uint32_t np;          // partitions
+  uint32_t chunks;      // batch chunks
+  uint32_t cap;         // fixed region size per partition (entries)
+};
+
+// Partitions the pipeline supports (LDS histogram of the counting kernel).
+constexpr uint32_t kMaxPartitions = 16384;
+constexpr uint32_t kPartBuckets = 256;
+constexpr uint32_t kPartChunk = 1024;
+
 void launch_init_slots(const TableView& t, uint64_t from_bucket,
                        uint64_t to_bucket, hipStream_t s);
 void launch_clear(const TableView& t, hipStream_t s);
@@ -60,6 +84,8 @@ void launch_erase(const TableView& t, const uint64_t* keys, uint64_t n,
                   hipStream_t s);
 void launch_apply(const TableView& t, int op, const ApplyArgs& a,
                   RouteScratch& rs, int parity, hipStream_t s);
+void launch_apply_part(const TableView& t, int op, const ApplyArgs& a,
+                       const PartScratch& ps, hipStream_t s);
 void launch_export(const TableView& t, uint64_t offset, uint64_t n,
                    uint64_t* d_counter, uint64_t* keys, uint8_t* values,
                    uint64_t* scores, uint32_t* block_scratch, int unit,

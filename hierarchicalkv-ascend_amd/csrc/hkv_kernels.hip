@@ -37,38 +37,65 @@ __global__ void k_init_slots(TableView t, uint64_t s0, uint64_t s1, uint64_t b0,
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
   for (uint64_t s = s0 + blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; s < s1;
        s += stride) {
-    t.digests[s] = kEmptyDigest;
-    t.keys[s] = kEmptyKey;
-    if (reset_scores) t.scores[s] = 0;
+    G(t.digests)[s] = kEmptyDigest;
+    if (reset_scores) slot_store(t, s, kEmptyKey, 0);
+    else slot_key(t, s) = kEmptyKey;
   }
   for (uint64_t b = b0 + blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; b < b1;
        b += stride)
-    t.bsize[b] = 0;
+    G(t.bsize)[b] = 0;
 }
 
 /* ------------------------------------------------------------------------ */
 /* find                                                                      */
 /* ------------------------------------------------------------------------ */
 
-// find_without_lock (include/find_utils.h:31-86): 4-digest groups from
-// align4(start) with wrap; digest matches are confirmed by the key; the first
-// EMPTY slot at or after `start` ends the search.  Digests are fetched 16
-// bytes at a time.
-__device__ __forceinline__ int probe_find(const TableView& t, uint64_t b,
-                                          uint32_t start, uint32_t d, uint64_t k) {
+// find_without_lock (include/find_utils.h:31-86): 4-slot groups from
+// align4(start) with wrap; in each group a slot holding the key is a hit, and
+// otherwise an EMPTY slot ends the search (in the first group only at or
+// after `start`).  The search visits B/4 + 1 groups, the first one twice.
+//
+// Two equivalent ways to test a group: compare the digests (one 16-byte load
+// covers four groups) and confirm matches with the key, or compare the four
+// keys of the group directly.  With `key_first` the groups that lie in
+// start's 128-byte line of slot records are tested by key (at load factors
+// well below 1 the search nearly always ends there, saving the digest line);
+// the rest of the search uses digests.  A slot's digest is the empty digest
+// exactly when its key is EMPTY, so both tests give the same answer.
+//
+// probe_find_from continues a search at group offset `off` (a multiple of 4).
+__device__ __forceinline__ int probe_find_from(const TableView& t, uint64_t b, uint32_t start,
+                                               uint32_t d, uint64_t k, bool key_first,
+                                               uint32_t off) {
   const uint32_t B = t.B;
-  const uint8_t* dg = t.digests + b * B;
-  const uint64_t* ks = t.keys + b * B;
+  const uint64_t base = b * B;
   const uint32_t a = start & ~3u;
+  if (key_first) {
+    // Groups a and, when a opens a line of 8 records, a + 4.
+    const uint32_t line_end = (a & 4u) ? 4u : 8u;
+    for (; off < line_end; off += 4) {
+      const uint32_t g = a + off;
+      uint32_t hit = kNone, empty = kNone;
+#pragma unroll
+      for (uint32_t j = 0; j < 4; j++) {
+        const uint64_t kj = slot_key(t, base + g + j);
+        if (kj == k && hit == kNone) hit = j;
+        if (kj == kEmptyKey && empty == kNone && (off != 0 || g + j >= start)) empty = j;
+      }
+      if (hit != kNone) return (int)(g + hit);
+      if (empty != kNone) return -1;
+    }
+  }
+  gptr<const uint8_t> dg = digest_row(t, b);
   const uint32_t rep = d * 0x01010101u;
   const uint32_t erep = (uint32_t)kEmptyDigest * 0x01010101u;
   uint32_t cur = kNone;
-  uint4 chunk = make_uint4(0, 0, 0, 0);
-  for (uint32_t off = 0; off < B + 4; off += 4) {
+  u32x4 chunk = {0, 0, 0, 0};
+  for (; off < B + 4; off += 4) {
     const uint32_t g = (a + off) & (B - 1);
     const uint32_t c = g >> 4;
     if (c != cur) {
-      chunk = *reinterpret_cast<const uint4*>(dg + (c << 4));
+      chunk = *(gptr<const u32x4>)(dg + (c << 4));
       cur = c;
     }
     const uint32_t wi = (g >> 2) & 3;
@@ -77,7 +104,7 @@ __device__ __forceinline__ int probe_find(const TableView& t, uint64_t b,
     while (m) {
       const uint32_t j = __builtin_ctz(m);
       m &= m - 1;
-      if (ks[g + j] == k) return (int)(g + j);
+      if (slot_key(t, base + g + j) == k) return (int)(g + j);
     }
     uint32_t e = eq_bytes4(w, erep);
     while (e) {
@@ -91,102 +118,173 @@ __device__ __forceinline__ int probe_find(const TableView& t, uint64_t b,
   return -1;
 }
 
-// Wave-cooperative copy of up to 64 rows.  `rows` lane ids are listed in
-// lds_rows; row r's source is `src` of lane lds_rows[r], its destination is
-// dst_base + (lane_base + lds_rows[r]) * row_bytes.
+__device__ __forceinline__ int probe_find(const TableView& t, uint64_t b, uint32_t start,
+                                          uint32_t d, uint64_t k, bool key_first) {
+  return probe_find_from(t, b, start, d, k, key_first, 0);
+}
+
+// Key-first probing pays off while the table is at most 3/4 full.
+__device__ __forceinline__ bool use_key_first(const TableView& t) {
+  return *G(t.live) * 4 < t.capacity * 3;
+}
+
+// Wave-cooperative copy of up to 64 rows.  Row r belongs to lane
+// lds_rows[r]: it is copied from that lane's `src` to
+// dst_base + (lane_base + lane) * row_bytes.  The wave is split into groups of
+// lpr lanes, one row per group; each pass moves four rows per group with all
+// loads issued before the stores.  Rows past `rows` load row lds_rows[0]
+// (valid) and store nothing.
 template <int U>
 __device__ __forceinline__ void wave_copy_rows(uint32_t rows, const uint32_t* lds_rows,
-                                               const uint8_t* src,
-                                               uint8_t* dst_base, uint64_t lane_base,
-                                               uint32_t row_bytes, bool src_is_out) {
+                                               gptr<const uint8_t> src, uint8_t* dst_base,
+                                               uint64_t lane_base, uint32_t row_bytes) {
   using T = typename UnitT<U>::T;
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t units = row_bytes / U;
   uint32_t lpr = 64;
   while (lpr > 1 && lpr / 2 >= units) lpr >>= 1;  // lanes per row
-  const uint32_t rpi = 64 / lpr;                    // rows per iteration
+  const uint32_t rpi = 64 / lpr;                    // rows per pass and quarter
   const uint32_t sub = lane % lpr;
+  const uint64_t sp = (uint64_t)(uintptr_t)src;
   for (uint32_t r0 = 0; r0 < rows; r0 += 4 * rpi) {
-    const T* s[4];
-    T* d[4];
-    bool ok[4];
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-      const uint32_t r = r0 + q * rpi + lane / lpr;
-      ok[q] = r < rows;
-      const uint32_t src_lane = ok[q] ? lds_rows[r] : lane;
-      const uint64_t sp = shfl_u64((uint64_t)(uintptr_t)src, (int)src_lane, 64);
-      const uint64_t row_index = lane_base + src_lane;
-      if (src_is_out) {
-        s[q] = reinterpret_cast<const T*>(dst_base + row_index * row_bytes);
-        d[q] = reinterpret_cast<T*>((uintptr_t)sp);
-      } else {
-        s[q] = reinterpret_cast<const T*>((uintptr_t)sp);
-        d[q] = reinterpret_cast<T*>(dst_base + row_index * row_bytes);
-      }
-    }
+    const uint32_t r = r0 + lane / lpr;
+    const bool ok0 = r < rows, ok1 = r + rpi < rows, ok2 = r + 2 * rpi < rows,
+               ok3 = r + 3 * rpi < rows;
+    const uint32_t l0 = lds_rows[ok0 ? r : 0], l1 = lds_rows[ok1 ? r + rpi : 0],
+                   l2 = lds_rows[ok2 ? r + 2 * rpi : 0], l3 = lds_rows[ok3 ? r + 3 * rpi : 0];
+    gptr<const T> s0 = G<const T>((uintptr_t)shfl_u64(sp, (int)l0, 64));
+    gptr<const T> s1 = G<const T>((uintptr_t)shfl_u64(sp, (int)l1, 64));
+    gptr<const T> s2 = G<const T>((uintptr_t)shfl_u64(sp, (int)l2, 64));
+    gptr<const T> s3 = G<const T>((uintptr_t)shfl_u64(sp, (int)l3, 64));
+    gptr<T> d0 = G(reinterpret_cast<T*>(dst_base + (lane_base + l0) * row_bytes));
+    gptr<T> d1 = G(reinterpret_cast<T*>(dst_base + (lane_base + l1) * row_bytes));
+    gptr<T> d2 = G(reinterpret_cast<T*>(dst_base + (lane_base + l2) * row_bytes));
+    gptr<T> d3 = G(reinterpret_cast<T*>(dst_base + (lane_base + l3) * row_bytes));
     for (uint32_t u = sub; u < units; u += lpr) {
-      T v[4];
-#pragma unroll
-      for (int q = 0; q < 4; q++)
-        if (ok[q]) v[q] = s[q][u];
-#pragma unroll
-      for (int q = 0; q < 4; q++)
-        if (ok[q]) d[q][u] = v[q];
+      const T v0 = s0[u], v1 = s1[u], v2 = s2[u], v3 = s3[u];
+      if (ok0) d0[u] = v0;
+      if (ok1) d1[u] = v1;
+      if (ok2) d2[u] = v2;
+      if (ok3) d3[u] = v3;
     }
   }
 }
 
-template <int U, bool MISSED>
-__global__ __launch_bounds__(kBlock) void k_find(TableView t, const uint64_t* __restrict__ keys,
-                                                 uint64_t n, uint8_t* __restrict__ values,
-                                                 uint8_t* __restrict__ founds,
-                                                 uint64_t* __restrict__ scores,
-                                                 uint64_t* __restrict__ missed_keys,
-                                                 int32_t* __restrict__ missed_idx,
-                                                 int32_t* __restrict__ missed_size) {
-  __shared__ uint32_t s_rows[kBlock / 64][64];
+// First step of a key-first search: load the four keys of the key's first
+// group.  find_tail recomputes the hash and completes the search.
+struct FindHead {
+  uint64_t k;
+  uint64_t g0, g1, g2, g3;
+  bool valid;
+};
+
+struct KeyPos {
+  uint64_t b;
+  uint32_t start, d;
+};
+
+__device__ __forceinline__ KeyPos key_pos(const TableView& t, uint64_t k) {
+  const uint64_t h = murmur3(k);
+  const uint64_t gi = global_idx(t, h);
+  return KeyPos{gi >> t.bshift, (uint32_t)(gi & (t.B - 1)), key_digest(h)};
+}
+
+__device__ __forceinline__ void find_head(const TableView& t, FindHead& f, uint64_t k,
+                                          bool valid, bool kf) {
+  f.k = k;
+  f.valid = valid && !is_reserved(k);
+  f.g0 = f.g1 = f.g2 = f.g3 = 0;
+  if (f.valid && kf) {
+    const KeyPos q = key_pos(t, k);
+    gptr<const uint64_t> rec = G(t.slots) + 2 * (q.b * t.B + (q.start & ~3u));
+    f.g0 = rec[0];
+    f.g1 = rec[2];
+    f.g2 = rec[4];
+    f.g3 = rec[6];
+  }
+}
+
+// Slot of the key (bucket in *b), or -1.
+__device__ __forceinline__ int find_tail(const TableView& t, const FindHead& f, bool kf,
+                                         uint64_t* b) {
+  if (!f.valid) return -1;
+  const KeyPos q = key_pos(t, f.k);
+  *b = q.b;
+  if (!kf) return probe_find(t, q.b, q.start, q.d, f.k, false);
+  const uint32_t a = q.start & ~3u;
+  if (f.g0 == f.k) return (int)a;
+  if (f.g1 == f.k) return (int)a + 1;
+  if (f.g2 == f.k) return (int)a + 2;
+  if (f.g3 == f.k) return (int)a + 3;
+  const uint32_t r = q.start - a;  // EMPTY slots before start do not end the search
+  if ((f.g0 == kEmptyKey && r == 0) || (f.g1 == kEmptyKey && r <= 1) ||
+      (f.g2 == kEmptyKey && r <= 2) || f.g3 == kEmptyKey)
+    return -1;
+  return probe_find_from(t, q.b, q.start, q.d, f.k, true, 4);
+}
+
+// One key per lane; the wave copies its hit rows.  Find is bound by HBM
+// traffic (a 128-byte metadata line plus the row in and out per hit), so more
+// work per wave does not help.  The missed-keys variant runs 1024-thread
+// blocks and appends a block's missed keys, collected in LDS, with one
+// atomic.
+template <int U, bool MISSED, int BLK>
+__global__ __launch_bounds__(BLK) void k_find(TableView t, const uint64_t* __restrict__ keys,
+                                              uint64_t n, uint8_t* __restrict__ values,
+                                              uint8_t* __restrict__ founds,
+                                              uint64_t* __restrict__ scores,
+                                              uint64_t* __restrict__ missed_keys,
+                                              int32_t* __restrict__ missed_idx,
+                                              int32_t* __restrict__ missed_size) {
+  constexpr uint32_t kMissCap = MISSED ? BLK : 1;
+  __shared__ uint32_t s_rows[BLK / 64][64];
+  __shared__ uint64_t s_mkey[kMissCap];
+  __shared__ uint32_t s_midx[kMissCap];
+  __shared__ uint32_t s_mcnt, s_mbase;
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t wv = threadIdx.x >> 6;
-  const uint64_t wave_base = (uint64_t)blockIdx.x * kBlock + wv * 64;
-  const uint64_t i = wave_base + lane;
-  bool found = false;
-  const uint8_t* src = nullptr;
-  uint64_t k = 0;
-  if (i < n) {
-    k = keys[i];
-    if (!is_reserved(k)) {
-      const uint64_t h = murmur3(k);
-      const uint64_t gi = global_idx(t, h);
-      const uint64_t b = gi >> t.bshift;
-      const uint32_t start = (uint32_t)(gi & (t.B - 1));
-      const int p = probe_find(t, b, start, key_digest(h), k);
-      if (p >= 0) {
-        found = true;
-        src = row_ptr(t, b, (uint32_t)p);
-        if (scores) scores[i] = t.scores[b * t.B + p];
-      }
+  const bool kf = use_key_first(t);
+  if (MISSED && threadIdx.x == 0) s_mcnt = 0;
+  if (MISSED) __syncthreads();
+  const uint64_t base0 = ((uint64_t)blockIdx.x * (BLK / 64) + wv) * 64;
+  const uint64_t i0 = base0 + lane;
+  FindHead f0;
+  find_head(t, f0, i0 < n ? keys[i0] : 0, i0 < n, kf);
+  auto finish = [&](const FindHead& f, uint64_t wave_base) __attribute__((always_inline)) {
+    const uint64_t i = wave_base + lane;
+    uint64_t b = 0;
+    const int p = find_tail(t, f, kf, &b);
+    const bool found = p >= 0;
+    gptr<const uint8_t> src = nullptr;
+    if (found) {
+      src = row_ptr(t, b, (uint32_t)p);
+      if (scores) scores[i] = slot_score(t, b * t.B + p);
     }
-    if (!MISSED && founds) founds[i] = found ? 1 : 0;
-  }
+    if (!MISSED && founds && i < n) founds[i] = found ? 1 : 0;
+    if (MISSED && i < n && !found) {
+      const uint32_t r = atomicAdd(&s_mcnt, 1u);
+      s_mkey[r] = f.k;
+      s_midx[r] = (uint32_t)i;
+    }
+    const uint64_t hm = __ballot(found);
+    if (found) s_rows[wv][__popcll(hm & ((1ull << lane) - 1))] = lane;
+    __builtin_amdgcn_wave_barrier();
+    const uint32_t rows = __popcll(hm);
+    if (rows) wave_copy_rows<U>(rows, s_rows[wv], src, values, wave_base, t.row_bytes);
+    __builtin_amdgcn_wave_barrier();
+  };
+  finish(f0, base0);
   if (MISSED) {
-    const bool miss = (i < n) && !found;
-    const uint64_t m = __ballot(miss);
-    const uint32_t cnt = __popcll(m);
-    uint32_t base = 0;
-    if (lane == 0 && cnt) base = atomicAdd(reinterpret_cast<uint32_t*>(missed_size), cnt);
-    base = __shfl(base, 0);
-    if (miss) {
-      const uint32_t r = __popcll(m & ((1ull << lane) - 1));
-      missed_keys[base + r] = k;
-      missed_idx[base + r] = (int32_t)i;
+    __syncthreads();
+    const uint32_t cnt = s_mcnt;
+    if (threadIdx.x == 0 && cnt)
+      s_mbase = atomicAdd(reinterpret_cast<uint32_t*>(missed_size), cnt);
+    __syncthreads();
+    for (uint32_t r = threadIdx.x; r < cnt; r += BLK) {
+      missed_keys[s_mbase + r] = s_mkey[r];
+      missed_idx[s_mbase + r] = (int32_t)s_midx[r];
     }
   }
-  const uint64_t hm = __ballot(found);
-  if (found) s_rows[wv][__popcll(hm & ((1ull << lane) - 1))] = lane;
-  __syncthreads();
-  const uint32_t rows = __popcll(hm);
-  if (rows) wave_copy_rows<U>(rows, s_rows[wv], src, values, wave_base, t.row_bytes, false);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -197,40 +295,46 @@ __global__ __launch_bounds__(kBlock) void k_find(TableView t, const uint64_t* __
 // is scanned (no early stop); a matching key becomes RECLAIM with score 0
 // and the reclaim digest.  The slot is claimed with a CAS so that a key
 // repeated in one batch is erased once, as if applied in batch order.
-__global__ __launch_bounds__(kBlock) void k_erase(TableView t, const uint64_t* __restrict__ keys,
-                                                  uint64_t n) {
-  const uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
-  if (i >= n) return;
-  const uint64_t k = keys[i];
-  if (is_reserved(k)) return;
+__device__ __forceinline__ bool erase_key(const TableView& t, uint64_t k) {
+  if (is_reserved(k)) return false;
   const uint32_t B = t.B;
   const uint64_t h = murmur3(k);
   const uint64_t gi = global_idx(t, h);
   const uint64_t b = gi >> t.bshift;
   const uint32_t start = (uint32_t)(gi & (B - 1));
   const uint32_t rep = key_digest(h) * 0x01010101u;
-  uint8_t* dg = t.digests + b * B;
-  uint64_t* ks = t.keys + b * B;
+  gptr<uint8_t> dg = digest_row(t, b);
   const uint32_t a = start & ~3u;
+  bool erased = false;
   for (uint32_t off = 0; off < B + 4; off += 4) {
     const uint32_t g = (a + off) & (B - 1);
-    const uint32_t w = *reinterpret_cast<const uint32_t*>(dg + g);
+    const uint32_t w = *(gptr<const uint32_t>)(dg + g);
     uint32_t m = eq_bytes4(w, rep);
     while (m) {
       const uint32_t j = __builtin_ctz(m);
       m &= m - 1;
-      if (ks[g + j] == k) {
-        if (atomicCAS(reinterpret_cast<unsigned long long*>(ks + g + j),
-                      (unsigned long long)k, (unsigned long long)kReclaimKey) ==
-            (unsigned long long)k) {
-          t.scores[b * B + g + j] = 0;
+      g64& key = slot_key(t, b * B + g + j);
+      if (key == k) {
+        if (atomicCAS((unsigned long long*)&key, (unsigned long long)k,
+                      (unsigned long long)kReclaimKey) == (unsigned long long)k) {
+          slot_score(t, b * B + g + j) = 0;
           dg[g + j] = kReclaimDigest;
           atomicSub(t.bsize + b, 1);
+          erased = true;
         }
         break;
       }
     }
   }
+  return erased;
+}
+
+__global__ __launch_bounds__(kBlock) void k_erase(TableView t, const uint64_t* __restrict__ keys,
+                                                  uint64_t n) {
+  const uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
+  const bool erased = i < n && erase_key(t, keys[i]);
+  const uint64_t m = __ballot(erased);
+  if ((threadIdx.x & 63) == 0 && m) atomicAdd(t.live, 0ull - (unsigned long long)__popcll(m));
 }
 
 /* ------------------------------------------------------------------------ */
@@ -286,12 +390,12 @@ __device__ __forceinline__ void bucket_load(const TableView& t, Bucket16& S, uin
   S.b = b;
   S.base = b * (uint64_t)t.B;
   S.l = l;
-  const uint8_t* dg = t.digests + S.base + l;
+  gptr<const uint8_t> dg = G(t.digests) + S.base + l;
   S.dg0 = (uint32_t)dg[0] | ((uint32_t)dg[16] << 8) | ((uint32_t)dg[32] << 16) |
           ((uint32_t)dg[48] << 24);
   S.dg1 = (uint32_t)dg[64] | ((uint32_t)dg[80] << 8) | ((uint32_t)dg[96] << 16) |
           ((uint32_t)dg[112] << 24);
-  S.bsz = S.bsz0 = t.bsize[b];
+  S.bsz = S.bsz0 = G(t.bsize)[b];
 }
 
 // Group-wide minimum of (score, rank) carrying the slot and its key.
@@ -313,10 +417,10 @@ __device__ __forceinline__ void group_min_victim(uint64_t& s, uint32_t& rank, ui
 }
 
 template <typename V>
-__device__ __forceinline__ void accum_units(uint8_t* dst, const uint8_t* delta, uint32_t bytes,
-                                            uint32_t r, uint32_t nl) {
-  V* d = reinterpret_cast<V*>(dst);
-  const V* s = reinterpret_cast<const V*>(delta);
+__device__ __forceinline__ void accum_units(gptr<uint8_t> dst, gptr<const uint8_t> delta,
+                                            uint32_t bytes, uint32_t r, uint32_t nl) {
+  gptr<V> d = (gptr<V>)dst;
+  gptr<const V> s = (gptr<const V>)delta;
   const uint32_t cntv = bytes / sizeof(V);
   for (uint32_t u = r; u < cntv; u += nl) {
     V v = s[u];
@@ -325,8 +429,8 @@ __device__ __forceinline__ void accum_units(uint8_t* dst, const uint8_t* delta, 
   }
 }
 
-__device__ __forceinline__ void accum_row(uint8_t* dst, const uint8_t* delta, uint32_t bytes,
-                                          int vt, uint32_t r, uint32_t nl) {
+__device__ __forceinline__ void accum_row(gptr<uint8_t> dst, gptr<const uint8_t> delta,
+                                          uint32_t bytes, int vt, uint32_t r, uint32_t nl) {
   switch (vt) {
     case 0: accum_units<float>(dst, delta, bytes, r, nl); break;           // f32
     case 8: accum_units<int32_t>(dst, delta, bytes, r, nl); break;         // i32
@@ -341,26 +445,24 @@ __device__ __forceinline__ void accum_row(uint8_t* dst, const uint8_t* delta, ui
 // (find_utils.h:94-227) with its callers (non-unique keys and accum).
 template <int OP, int U>
 __device__ __forceinline__ void apply_key(const TableView& t, Bucket16& S, const ApplyArgs& a,
-                                          uint64_t i) {
+                                          uint64_t i, uint64_t k) {
   constexpr int SPL = 8;
   const uint32_t B = t.B;
   const uint32_t l = S.l;
-  const uint64_t k = a.keys[i];
   const bool has_in = a.in_scores != nullptr;
-  const uint64_t in = has_in ? a.in_scores[i] : 0;
+  const uint64_t in = has_in ? G(a.in_scores)[i] : 0;
   const uint64_t h = murmur3(k);
   const uint64_t gi = global_idx(t, h);
   const uint32_t start = (uint32_t)(gi & (B - 1));
   const uint32_t d = key_digest(h);
   const uint64_t des = score_desired(a.sc, has_in, in);
-  const uint64_t* kp = t.keys + S.base + l;
 
   // 1. Is the key present?  Candidates are digest matches.
   const uint32_t a4 = start & ~3u;
   uint32_t best = kNone;
 #pragma unroll
   for (int j = 0; j < SPL; j++) {
-    if (dg_of(S, j) == d && kp[16 * j] == k) {
+    if (dg_of(S, j) == d && slot_key(t, S.base + l + 16 * j) == k) {
       const uint32_t p = l + 16 * j;
       const uint32_t rk = (((p - a4) & (B - 1)) << 8) | p;
       best = rk < best ? rk : best;
@@ -395,14 +497,14 @@ __device__ __forceinline__ void apply_key(const TableView& t, Bucket16& S, const
     }
     if (res == 0) {
       // 3. Eviction over every slot of the bucket.
-      const uint64_t* sp = t.scores + S.base + l;
       uint64_t ms = kMaxScore, mk = 0;
       uint32_t mr = kNone, mp = start;
 #pragma unroll
       for (int j = 0; j < SPL; j++) {
         const uint32_t p = l + 16 * j;
-        const uint64_t kj = kp[16 * j];
-        const uint64_t sj = sp[16 * j];
+        const u64x2 rec = slot_load(t, S.base + p);
+        const uint64_t kj = rec.x;
+        const uint64_t sj = rec.y;
         uint32_t rank;
         bool elig;
         if (a.rule == RULE_DIGEST16) {
@@ -429,7 +531,7 @@ __device__ __forceinline__ void apply_key(const TableView& t, Bucket16& S, const
         // Every eligible score is MAX_SCORE: the start slot is taken.
         mp = start;
         uint64_t kk = 0;
-        if (l == (start & 15u)) kk = t.keys[S.base + start];
+        if (l == (start & 15u)) kk = slot_key(t, S.base + start);
         mk = shfl_u64(kk, (int)(start & 15u), 16);
       }
       if (des < ms) {
@@ -445,10 +547,10 @@ __device__ __forceinline__ void apply_key(const TableView& t, Bucket16& S, const
 
   // 4. Effects.
   const uint32_t R = t.row_bytes;
-  const uint8_t* in_row = a.in_values ? a.in_values + i * (uint64_t)R : nullptr;
+  gptr<const uint8_t> in_row = a.in_values ? G(a.in_values) + i * (uint64_t)R : nullptr;
   if (OP == OP_ACCUM_OR_ASSIGN) {
     if (res == R_REFUSED) return;
-    const bool is_accum = a.accum_flags[i] != 0;
+    const bool is_accum = G(a.accum_flags)[i] != 0;
     if ((is_accum && res != R_DUP) || (!is_accum && res == R_DUP)) return;
   }
   if (res == R_REFUSED) {
@@ -457,29 +559,29 @@ __device__ __forceinline__ void apply_key(const TableView& t, Bucket16& S, const
       if (l == 0) j = atomicAdd(reinterpret_cast<unsigned long long*>(a.ev_counter), 1ull);
       j = shfl_u64(j, 0, 16);
       if (l == 0) {
-        a.ev_keys[j] = k;
-        if (a.ev_scores) a.ev_scores[j] = des;
+        G(a.ev_keys)[j] = k;
+        if (a.ev_scores) G(a.ev_scores)[j] = des;
       }
-      copy_units<U>(a.ev_values + j * R, in_row, R, l, 16);
+      copy_units<U>(G(a.ev_values) + j * R, in_row, R, l, 16);
     }
     return;
   }
-  uint8_t* trow = row_ptr(t, S.b, pos);
+  gptr<uint8_t> trow = row_ptr(t, S.b, pos);
   if (OP == OP_INSERT_AND_EVICT && res == R_EVICT) {
     uint64_t j = 0;
     if (l == 0) j = atomicAdd(reinterpret_cast<unsigned long long*>(a.ev_counter), 1ull);
     j = shfl_u64(j, 0, 16);
     if (l == 0) {
-      a.ev_keys[j] = victim_key;
-      if (a.ev_scores) a.ev_scores[j] = victim_score;
+      G(a.ev_keys)[j] = victim_key;
+      if (a.ev_scores) G(a.ev_scores)[j] = victim_score;
     }
-    copy_units<U>(a.ev_values + j * R, trow, R, l, 16);
+    copy_units<U>(G(a.ev_values) + j * R, trow, R, l, 16);
   }
   if (res == R_EMPTY || res == R_RECLAIMED) S.bsz++;
 
   if (res == R_DUP) {
     if (OP == OP_FIND_OR_INSERT) {
-      copy_units<U>(a.io_values + i * (uint64_t)R, trow, R, l, 16);
+      copy_units<U>(G(a.io_values) + i * (uint64_t)R, trow, R, l, 16);
     } else if (OP == OP_ACCUM_OR_ASSIGN) {
       accum_row(trow, in_row, R, a.value_type, l, 16);
     } else if (OP != OP_ASSIGN_SCORES) {
@@ -493,7 +595,9 @@ __device__ __forceinline__ void apply_key(const TableView& t, Bucket16& S, const
   if (l == owner) {
     uint64_t old = 0;
     if (res == R_DUP && (a.sc.strategy == kLfu || a.sc.strategy == kEpochLfu))
-      old = t.scores[S.base + pos];
+      old = slot_score(t, S.base + pos);
+    else if (res != R_DUP && a.sc.strategy == kLfu && !has_in)
+      old = slot_score(t, S.base + pos);
     bool w;
     uint64_t ns;
     if (OP == OP_ASSIGN_SCORES) {
@@ -503,19 +607,23 @@ __device__ __forceinline__ void apply_key(const TableView& t, Bucket16& S, const
     } else {
       ns = score_new(a.sc, has_in, in, des, old, &w);
     }
-    if (w) {
-      t.scores[S.base + pos] = ns;
-      if (res != R_DUP) {
-        t.digests[S.base + pos] = (uint8_t)d;
-        dg_set(S, jj, d);
-      }
+    if (res == R_DUP) {
+      if (w) slot_score(t, S.base + pos) = ns;
+    } else if (w) {
+      slot_store(t, S.base + pos, k, ns);
+      G(t.digests)[S.base + pos] = (uint8_t)d;
+      dg_set(S, jj, d);
+    } else {
+      slot_key(t, S.base + pos) = k;
     }
-    if (res != R_DUP) t.keys[S.base + pos] = k;
   }
 }
 
 __device__ __forceinline__ void bucket_finish(const TableView& t, Bucket16& S) {
-  if (S.l == 0 && S.bsz != S.bsz0) t.bsize[S.b] = S.bsz;
+  if (S.l == 0 && S.bsz != S.bsz0) {
+    G(t.bsize)[S.b] = S.bsz;
+    atomicAdd(t.live, (unsigned long long)(int64_t)(S.bsz - S.bsz0));
+  }
 }
 
 // Pending-count word after the lane-per-bucket pass: bits 0-15 hold the
@@ -543,8 +651,8 @@ __device__ __forceinline__ void flush_tasks(uint32_t ntask, const uint64_t* s_sr
   // Rows beyond ntask read task 0's source (valid) and store nothing.
   const uint64_t any_src = s_src[0] & ~kAccumBit;
   for (uint32_t r0 = 0; r0 < ntask; r0 += Q * rpi) {
-    const T* s[Q];
-    T* d[Q];
+    gptr<const T> s[Q];
+    gptr<T> d[Q];
 #pragma unroll
     for (int q = 0; q < Q; q++) {
       const uint32_t r = r0 + q * rpi + lane / lpr;
@@ -552,12 +660,12 @@ __device__ __forceinline__ void flush_tasks(uint32_t ntask, const uint64_t* s_sr
       uint64_t dp = ok ? s_dst[r] : 0;
       const uint64_t sp = ok ? s_src[r] : any_src;
       if (dp & kAccumBit) {
-        accum_row(reinterpret_cast<uint8_t*>((uintptr_t)(dp & ~kAccumBit)),
-                  reinterpret_cast<const uint8_t*>((uintptr_t)sp), row_bytes, vt, sub, lpr);
+        accum_row(G<uint8_t>((uintptr_t)(dp & ~kAccumBit)), G<const uint8_t>((uintptr_t)sp),
+                  row_bytes, vt, sub, lpr);
         dp = 0;
       }
-      s[q] = reinterpret_cast<const T*>((uintptr_t)(dp ? sp : any_src));
-      d[q] = reinterpret_cast<T*>((uintptr_t)dp);
+      s[q] = G<const T>((uintptr_t)(dp ? sp : any_src));
+      d[q] = G<T>((uintptr_t)dp);
     }
     for (uint32_t u = sub; u < units; u += lpr) {
       if constexpr (Q == 2) {
@@ -592,18 +700,17 @@ __device__ __forceinline__ void flush_tasks(uint32_t ntask, const uint64_t* s_sr
 __device__ __forceinline__ int probe_upsert(const TableView& t, uint64_t base, uint32_t start,
                                             uint32_t d, uint64_t k, bool not_full, int* dup) {
   const uint32_t B = t.B;
-  const uint8_t* dg = t.digests + base;
-  const uint64_t* ks = t.keys + base;
+  gptr<const uint8_t> dg = G(t.digests) + base;
   const uint32_t a = start & ~3u;
   const uint32_t rep = d * 0x01010101u;
   const uint32_t erep = (uint32_t)kEmptyDigest * 0x01010101u;
   uint32_t cur = kNone;
-  uint4 chunk = make_uint4(0, 0, 0, 0);
+  u32x4 chunk = {0, 0, 0, 0};
   for (uint32_t off = 0; off < B + 4; off += 4) {
     const uint32_t g = (a + off) & (B - 1);
     const uint32_t c = g >> 4;
     if (c != cur) {
-      chunk = *reinterpret_cast<const uint4*>(dg + (c << 4));
+      chunk = *(gptr<const u32x4>)(dg + (c << 4));
       cur = c;
     }
     const uint32_t wi = (g >> 2) & 3;
@@ -612,7 +719,7 @@ __device__ __forceinline__ int probe_upsert(const TableView& t, uint64_t base, u
     while (m) {
       const uint32_t j = __builtin_ctz(m);
       m &= m - 1;
-      if (ks[g + j] == k) {
+      if (slot_key(t, base + g + j) == k) {
         *dup = 1;
         return (int)(g + j);
       }
@@ -629,6 +736,247 @@ __device__ __forceinline__ int probe_upsert(const TableView& t, uint64_t base, u
     }
   }
   return -1;
+}
+
+// The digest line of one bucket (128 digests, slot s in byte s) held in
+// registers by the lane that owns the bucket, so that its probes read no
+// memory: the lane is the bucket's only writer and keeps the copy current.
+struct DLine {
+  u32x4 c0, c1, c2, c3, c4, c5, c6, c7;
+};
+
+__device__ __forceinline__ void dl_load(DLine& L, gptr<const uint8_t> dg) {
+  gptr<const u32x4> q = (gptr<const u32x4>)dg;
+  L.c0 = q[0];
+  L.c1 = q[1];
+  L.c2 = q[2];
+  L.c3 = q[3];
+  L.c4 = q[4];
+  L.c5 = q[5];
+  L.c6 = q[6];
+  L.c7 = q[7];
+}
+
+// Chunk c of the line.  Written as mask arithmetic rather than a chain of
+// selects, which the compiler would turn into an indexed stack array.
+__device__ __forceinline__ u32x4 dl_chunk(const DLine& L, uint32_t c) {
+  const uint32_t m0 = 0u - (c == 0), m1 = 0u - (c == 1), m2 = 0u - (c == 2),
+                 m3 = 0u - (c == 3), m4 = 0u - (c == 4), m5 = 0u - (c == 5),
+                 m6 = 0u - (c == 6), m7 = 0u - (c == 7);
+  return (L.c0 & m0) | (L.c1 & m1) | (L.c2 & m2) | (L.c3 & m3) | (L.c4 & m4) | (L.c5 & m5) |
+         (L.c6 & m6) | (L.c7 & m7);
+}
+
+// Digests of the 4-slot group starting at slot g (g % 4 == 0).
+__device__ __forceinline__ uint32_t dl_word(const DLine& L, uint32_t g) {
+  const u32x4 ch = dl_chunk(L, g >> 4);
+  const uint32_t wi = (g >> 2) & 3;
+  return wi == 0 ? ch.x : wi == 1 ? ch.y : wi == 2 ? ch.z : ch.w;
+}
+
+__device__ __forceinline__ void dl_set(DLine& L, uint32_t p, uint32_t d) {
+  const uint32_t c = p >> 4, wi = (p >> 2) & 3, sh = 8 * (p & 3);
+  const uint32_t keep = ~(0xFFu << sh), v = d << sh;
+  // Byte p of the line: clear it and or in d, in every chunk under a mask
+  // that is all ones only for chunk c and word wi.
+  u32x4 km, vm;
+  km.x = wi == 0 ? keep : ~0u;
+  km.y = wi == 1 ? keep : ~0u;
+  km.z = wi == 2 ? keep : ~0u;
+  km.w = wi == 3 ? keep : ~0u;
+  vm.x = wi == 0 ? v : 0u;
+  vm.y = wi == 1 ? v : 0u;
+  vm.z = wi == 2 ? v : 0u;
+  vm.w = wi == 3 ? v : 0u;
+#define HKV_DL_SET(CC, N)                   \
+  {                                         \
+    const uint32_t on = 0u - (c == N);      \
+    L.CC = (L.CC & (km | ~on)) | (vm & on); \
+  }
+  HKV_DL_SET(c0, 0)
+  HKV_DL_SET(c1, 1)
+  HKV_DL_SET(c2, 2)
+  HKV_DL_SET(c3, 3)
+  HKV_DL_SET(c4, 4)
+  HKV_DL_SET(c5, 5)
+  HKV_DL_SET(c6, 6)
+  HKV_DL_SET(c7, 7)
+#undef HKV_DL_SET
+}
+
+// probe_upsert on a register digest line.
+__device__ __forceinline__ int probe_upsert_reg(const TableView& t, const DLine& L,
+                                                uint64_t base, uint32_t start, uint32_t d,
+                                                uint64_t k, bool not_full, int* dup) {
+  const uint32_t B = t.B;
+  const uint32_t a = start & ~3u;
+  const uint32_t rep = d * 0x01010101u;
+  const uint32_t erep = (uint32_t)kEmptyDigest * 0x01010101u;
+  for (uint32_t off = 0; off < B + 4; off += 4) {
+    const uint32_t g = (a + off) & (B - 1);
+    const uint32_t w = dl_word(L, g);
+    uint32_t m = eq_bytes4(w, rep);
+    while (m) {
+      const uint32_t j = __builtin_ctz(m);
+      m &= m - 1;
+      if (slot_key(t, base + g + j) == k) {
+        *dup = 1;
+        return (int)(g + j);
+      }
+    }
+    if (!not_full) continue;
+    uint32_t e = eq_bytes4(w, erep);
+    while (e) {
+      const uint32_t j = __builtin_ctz(e);
+      e &= e - 1;
+      const uint32_t p = g + j;
+      if (off == 0 && p < start) continue;
+      *dup = 0;
+      return (int)p;
+    }
+  }
+  return -1;
+}
+
+// Workgroup barrier that orders LDS only (global stores stay in flight).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// probe_upsert on a copy of the bucket's digests in LDS (`dg` = 32 words, the
+// digests of slots 4w..4w+3 in word w), kept current by the bucket's owner.
+__device__ __forceinline__ int probe_upsert_lds(const TableView& t, const uint32_t* dg,
+                                                uint64_t base, uint32_t start, uint32_t d,
+                                                uint64_t k, bool not_full, int* dup) {
+  const uint32_t B = t.B;
+  const uint32_t a = start & ~3u;
+  const uint32_t rep = d * 0x01010101u;
+  const uint32_t erep = (uint32_t)kEmptyDigest * 0x01010101u;
+  for (uint32_t off = 0; off < B + 4; off += 4) {
+    const uint32_t g = (a + off) & (B - 1);
+    const uint32_t w = dg[g >> 2];
+    uint32_t m = eq_bytes4(w, rep);
+    while (m) {
+      const uint32_t j = __builtin_ctz(m);
+      m &= m - 1;
+      if (slot_key(t, base + g + j) == k) {
+        *dup = 1;
+        return (int)(g + j);
+      }
+    }
+    if (!not_full) continue;
+    uint32_t e = eq_bytes4(w, erep);
+    while (e) {
+      const uint32_t j = __builtin_ctz(e);
+      e &= e - 1;
+      const uint32_t p = g + j;
+      if (off == 0 && p < start) continue;
+      *dup = 0;
+      return (int)p;
+    }
+  }
+  return -1;
+}
+
+// Result bits of lane_apply.
+constexpr uint32_t kLaneDigest = 1;  // a new key's digest was written at the slot
+constexpr uint32_t kLaneRead = 2;    // the task reads the table row (a find_or_insert hit)
+
+// Effects of one key whose probe returned slot p (dup: the key is present),
+// for the lane that owns the bucket (`base` = its first slot, `rows0` = the
+// row of its slot 0).  Metadata is updated in place; the row movement is
+// returned as a task (*src -> *dst, dst = 0 for none; an accumulate task has
+// kAccumBit set in dst).
+template <int OP>
+__device__ __forceinline__ uint32_t lane_apply(const TableView& t, const ApplyArgs& a,
+                                               uint64_t base, gptr<uint8_t> rows0, int p,
+                                               int dup, uint64_t i, uint64_t k, uint64_t in,
+                                               bool has_in, uint32_t d, int32_t& bsz,
+                                               uint64_t& src, uint64_t& dst) {
+  const uint32_t R = t.row_bytes;
+  src = dst = 0;
+  const uint64_t des = score_desired(a.sc, has_in, in);
+  if (OP == OP_ACCUM_OR_ASSIGN) {
+    const bool is_accum = G(a.accum_flags)[i] != 0;
+    if (is_accum != (dup != 0)) return 0;
+  }
+  gptr<uint8_t> trow = rows0 + (uint64_t)p * R;
+  gptr<const uint8_t> in_row = a.in_values ? G(a.in_values) + i * (uint64_t)R : nullptr;
+  bool w;
+  uint32_t res = 0;
+  if (dup) {
+    uint64_t old = 0;
+    if (a.sc.strategy == kLfu || a.sc.strategy == kEpochLfu) old = slot_score(t, base + p);
+    const uint64_t ns = OP == OP_ASSIGN_SCORES ? score_wo_missed(a.sc, has_in, in, old, &w)
+                                               : score_hit(a.sc, has_in, in, des, old, &w);
+    if (w) slot_score(t, base + p) = ns;
+    if (OP == OP_FIND_OR_INSERT) {
+      src = (uint64_t)(uintptr_t)trow;
+      dst = (uint64_t)(uintptr_t)(G(a.io_values) + i * (uint64_t)R);
+      res |= kLaneRead;
+    } else if (OP == OP_ACCUM_OR_ASSIGN) {
+      src = (uint64_t)(uintptr_t)in_row;
+      dst = (uint64_t)(uintptr_t)trow | kAccumBit;
+    } else if (OP != OP_ASSIGN_SCORES) {
+      src = (uint64_t)(uintptr_t)in_row;
+      dst = (uint64_t)(uintptr_t)trow;
+    }
+  } else {
+    // The old score matters only to Lfu without input scores.
+    const uint64_t old = (a.sc.strategy == kLfu && !has_in) ? slot_score(t, base + p) : 0;
+    const uint64_t ns = score_new(a.sc, has_in, in, des, old, &w);
+    if (w) {
+      slot_store(t, base + p, k, ns);
+      G(t.digests)[base + p] = (uint8_t)d;
+      res |= kLaneDigest;
+    } else {
+      slot_key(t, base + p) = k;
+    }
+    bsz++;
+    src = (uint64_t)(uintptr_t)in_row;
+    dst = (uint64_t)(uintptr_t)trow;
+  }
+  return res;
+}
+
+// One key applied by the lane that owns bucket b, probing the digests in
+// memory, unless it needs the eviction path: then nothing is changed and the
+// function returns false.  *slot is the slot of the key's task.
+template <int OP>
+__device__ __forceinline__ bool lane_step(const TableView& t, const ApplyArgs& a, uint64_t b,
+                                          uint64_t base, uint64_t i, uint64_t k, uint64_t in,
+                                          bool has_in, int32_t& bsz, uint64_t& src,
+                                          uint64_t& dst, int& slot) {
+  const uint32_t B = t.B;
+  const uint64_t h = murmur3(k);
+  const uint64_t gi = global_idx(t, h);
+  const uint32_t start = (uint32_t)(gi & (B - 1));
+  const uint32_t d = key_digest(h);
+  int dup = 0;
+  const bool may_insert = OP != OP_ASSIGN_SCORES;
+  const int p = probe_upsert(t, base, start, d, k, may_insert && bsz < (int32_t)B, &dup);
+  src = dst = 0;
+  slot = p;
+  if (p < 0) return !may_insert;  // absent keys are a no-op for assign_scores
+  lane_apply<OP>(t, a, base, row_ptr(t, b, 0), p, dup, i, k, in, has_in, d, bsz, src, dst);
+  return true;
+}
+
+// Marks `slot` in the per-lane set of slots whose row is queued for writing;
+// returns whether it was already marked (a second write must flush first so
+// that the later key wins).
+__device__ __forceinline__ bool mark_written(uint32_t& wr0, uint32_t& wr1, uint32_t& wr2,
+                                             uint32_t& wr3, int slot) {
+  const uint32_t bit = 1u << (slot & 31);
+  const uint32_t wq = (uint32_t)slot >> 5;
+  const uint32_t cur = wq == 0 ? wr0 : wq == 1 ? wr1 : wq == 2 ? wr2 : wr3;
+  wr0 |= wq == 0 ? bit : 0u;
+  wr1 |= wq == 1 ? bit : 0u;
+  wr2 |= wq == 2 ? bit : 0u;
+  wr3 |= wq == 3 ? bit : 0u;
+  return (cur & bit) != 0;
 }
 
 // Lane-per-bucket pass: each lane owns one bucket with 1..16 routed keys and
@@ -659,7 +1007,7 @@ __global__ __launch_bounds__(kBlock) void k_apply_lpb(TableView t, ApplyArgs a,
 #pragma unroll
   for (uint32_t q = 0; q < kLightMax; q++) e[q] = (light && q < c) ? pend[b * P + q] + 1u : 0u;
   const uint64_t base = b * (uint64_t)B;
-  int32_t bsz = light ? t.bsize[b] : 0;
+  int32_t bsz = light ? G(t.bsize)[b] : 0;
   const int32_t bsz0 = bsz;
   uint32_t maxc = light ? c : 0;
 #pragma unroll
@@ -681,8 +1029,8 @@ __global__ __launch_bounds__(kBlock) void k_apply_lpb(TableView t, ApplyArgs a,
     if (e[q] > 0 && e[q] < m_next) m_next = e[q];
   uint64_t k_next = 0, in_next = 0;
   if (light) {
-    k_next = a.keys[m_next - 1];
-    if (has_in) in_next = a.in_scores[m_next - 1];
+    k_next = G(a.keys)[m_next - 1];
+    if (has_in) in_next = G(a.in_scores)[m_next - 1];
   }
   for (uint32_t step = 0; step < maxc; step++) {
     uint64_t src = 0, dst = 0;
@@ -697,69 +1045,15 @@ __global__ __launch_bounds__(kBlock) void k_apply_lpb(TableView t, ApplyArgs a,
       for (uint32_t q = 0; q < kLightMax; q++)
         if (e[q] > m && e[q] < m_next) m_next = e[q];
       if (m_next != kNone) {
-        k_next = a.keys[m_next - 1];
-        if (has_in) in_next = a.in_scores[m_next - 1];
+        k_next = G(a.keys)[m_next - 1];
+        if (has_in) in_next = G(a.in_scores)[m_next - 1];
       }
-      const uint64_t h = murmur3(k);
-      const uint64_t gi = global_idx(t, h);
-      const uint32_t start = (uint32_t)(gi & (B - 1));
-      const uint32_t d = key_digest(h);
-      int dup = 0;
-      const bool may_insert = OP != OP_ASSIGN_SCORES;
-      const int p = probe_upsert(t, base, start, d, k, may_insert && bsz < (int32_t)B, &dup);
-      if (p < 0 && may_insert) {
+      int slot = -1;
+      if (!lane_step<OP>(t, a, b, base, i, k, in, has_in, bsz, src, dst, slot)) {
         active = false;  // eviction path: hand over from this key on
         stop = step;
-      } else if (p >= 0) {
-        const uint64_t des = score_desired(a.sc, has_in, in);
-        bool apply = true;
-        if (OP == OP_ACCUM_OR_ASSIGN) {
-          const bool is_accum = a.accum_flags[i] != 0;
-          apply = is_accum == (dup != 0);
-        }
-        if (apply) {
-          uint8_t* trow = row_ptr(t, b, (uint32_t)p);
-          const uint8_t* in_row = a.in_values ? a.in_values + i * (uint64_t)R : nullptr;
-          bool w;
-          if (dup) {
-            uint64_t old = 0;
-            if (a.sc.strategy == kLfu || a.sc.strategy == kEpochLfu) old = t.scores[base + p];
-            const uint64_t ns = OP == OP_ASSIGN_SCORES
-                                    ? score_wo_missed(a.sc, has_in, in, old, &w)
-                                    : score_hit(a.sc, has_in, in, des, old, &w);
-            if (w) t.scores[base + p] = ns;
-            if (OP == OP_FIND_OR_INSERT) {
-              src = (uint64_t)(uintptr_t)trow;
-              dst = (uint64_t)(uintptr_t)(a.io_values + i * (uint64_t)R);
-            } else if (OP == OP_ACCUM_OR_ASSIGN) {
-              src = (uint64_t)(uintptr_t)in_row;
-              dst = (uint64_t)(uintptr_t)trow | kAccumBit;
-            } else if (OP != OP_ASSIGN_SCORES) {
-              src = (uint64_t)(uintptr_t)in_row;
-              dst = (uint64_t)(uintptr_t)trow;
-            }
-          } else {
-            const uint64_t ns = score_new(a.sc, has_in, in, des, t.scores[base + p], &w);
-            if (w) {
-              t.scores[base + p] = ns;
-              t.digests[base + p] = (uint8_t)d;
-            }
-            t.keys[base + p] = k;
-            bsz++;
-            src = (uint64_t)(uintptr_t)in_row;
-            dst = (uint64_t)(uintptr_t)trow;
-          }
-          if (!kStepFlush && dst) {
-            const uint32_t bit = 1u << (p & 31);
-            const uint32_t wq = (uint32_t)p >> 5;
-            const uint32_t cur = wq == 0 ? wr0 : wq == 1 ? wr1 : wq == 2 ? wr2 : wr3;
-            conflict = (cur & bit) != 0;
-            wr0 |= wq == 0 ? bit : 0u;
-            wr1 |= wq == 1 ? bit : 0u;
-            wr2 |= wq == 2 ? bit : 0u;
-            wr3 |= wq == 3 ? bit : 0u;
-          }
-        }
+      } else if (!kStepFlush && dst) {
+        conflict = mark_written(wr0, wr1, wr2, wr3, slot);
       }
     }
     // Queue this step's row tasks; flush first when full or when a slot is
@@ -790,9 +1084,13 @@ __global__ __launch_bounds__(kBlock) void k_apply_lpb(TableView t, ApplyArgs a,
   __builtin_amdgcn_wave_barrier();
   if (ntask) flush_tasks<U, 8>(ntask, s_src[wv], s_dst[wv], R, a.value_type);
   if (light) {
-    if (bsz != bsz0) t.bsize[b] = bsz;
+    if (bsz != bsz0) G(t.bsize)[b] = bsz;
     cnt[b] = stop == c ? 0u : (kDefer | (stop << 16) | c);
   }
+  uint32_t added = (uint32_t)(bsz - bsz0);
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) added += __shfl_xor(added, m, 64);
+  if (lane == 0 && added) atomicAdd(t.live, (unsigned long long)added);
 }
 
 // One 16-lane group per bucket the lane pass did not finish: buckets with
@@ -827,7 +1125,7 @@ __global__ __launch_bounds__(kBlock) void k_apply(TableView t, ApplyArgs a,
       if (e[q] > last && e[q] < m) m = e[q];
     m = group_min_u32(m);
     last = m;
-    if (step >= first) apply_key<OP, U>(t, S, a, (uint64_t)(m - 1));
+    if (step >= first) apply_key<OP, U>(t, S, a, (uint64_t)(m - 1), G(a.keys)[m - 1]);
   }
   bucket_finish(t, S);
   if (l == 0) cnt[gid] = 0;
@@ -852,20 +1150,807 @@ __global__ __launch_bounds__(kBlock) void k_apply_heavy(TableView t, ApplyArgs a
     for (uint64_t base = 0; base < a.n; base += 16) {
       const uint64_t i = base + l;
       bool mine = false;
+      uint64_t k = 0;
       if (i < a.n) {
-        const uint64_t k = a.keys[i];
+        k = G(a.keys)[i];
         mine = !is_reserved(k) && (global_idx(t, murmur3(k)) >> t.bshift) == b;
       }
       uint32_t mask = (uint32_t)(__ballot(mine) >> (16 * gslot)) & 0xFFFFu;
       while (mask) {
         const uint32_t q = __builtin_ctz(mask);
         mask &= mask - 1;
-        apply_key<OP, U>(t, S, a, base + q);
+        apply_key<OP, U>(t, S, a, base + q, shfl_u64(k, (int)q, 16));
       }
     }
     bucket_finish(t, S);
     if (l == 0) cnt[b] = 0;
   }
+}
+
+/* ------------------------------------------------------------------------ */
+/* partitioned apply (all mutating batch operations)                         */
+/* ------------------------------------------------------------------------ */
+//
+// 1. k_pcount: per 2048-key chunk g of the batch, the number of keys of each
+//    partition p (256 consecutive buckets), counted in LDS.
+// 2. k_pscan: per partition, its total and the offset of every segment
+//    (g, p); partitions that fit their fixed region are placed there, larger
+//    ones in a spill area.  Segments of a partition are consecutive and in
+//    chunk order, so all keys of segment g precede those of g + 1 in batch
+//    order.
+// 3. k_pscatter: every key writes {key, batch index} into its segment.
+// 4. k_apply_part: one workgroup per partition.  It loads the partition's
+//    entries into LDS (in runs of whole segments when they do not fit at
+//    once), groups them by bucket, and applies each bucket's keys in batch
+//    order: first one lane per bucket while no eviction is needed, then one
+//    16-lane group per bucket that needs the eviction path or holds many keys.
+// No atomics touch table memory: a bucket has exactly one owner at a time.
+
+constexpr uint32_t kPartLds = kPartChunk;  // entries one LDS load holds
+constexpr uint32_t kDgStride = 33;         // words per bucket digest row in LDS
+constexpr uint32_t kLaneMax = 32;          // keys per bucket the lane pass takes
+constexpr uint32_t kPartTaskCap = 128;     // queued row tasks per wave
+
+__device__ __forceinline__ uint64_t bucket_of(const TableView& t, uint64_t k) {
+  return global_idx(t, murmur3(k)) >> t.bshift;
+}
+
+__global__ __launch_bounds__(kBlock) void k_pcount(TableView t, const uint64_t* __restrict__ keys,
+                                                   uint64_t n, PartScratch ps) {
+  extern __shared__ uint32_t s_h[];
+  const uint32_t NP = ps.np;
+  for (uint32_t q = threadIdx.x; q < NP; q += kBlock) s_h[q] = 0;
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    *ps.spill_top = 0;
+    ps.dctr[0] = 0;
+    ps.dctr[1] = 0;
+  }
+  __syncthreads();
+  const uint64_t i0 = (uint64_t)blockIdx.x * kPartChunk;
+  for (uint32_t j = threadIdx.x; j < kPartChunk; j += kBlock) {
+    const uint64_t i = i0 + j;
+    if (i < n) {
+      const uint64_t k = keys[i];
+      if (!is_reserved(k)) atomicAdd(&s_h[bucket_of(t, k) / kPartBuckets], 1u);
+    }
+  }
+  __syncthreads();
+  uint32_t* H = ps.hist + (uint64_t)blockIdx.x * NP;
+  for (uint32_t q = threadIdx.x; q < NP; q += kBlock) H[q] = s_h[q];
+}
+
+// 16 partitions per block of 1024 threads; thread (segment group sg, column
+// c) handles chunks [sg * per, (sg + 1) * per) of partition c, so that each
+// block row of 16 columns reads 64 contiguous bytes per chunk.
+constexpr uint32_t kScanGroups = 64;
+
+__global__ __launch_bounds__(1024) void k_pscan(PartScratch ps) {
+  __shared__ uint32_t s_part[kScanGroups][16];
+  __shared__ uint32_t s_base[16];
+  const uint32_t c = threadIdx.x & 15, sg = threadIdx.x >> 4;
+  const uint32_t p = blockIdx.x * 16 + c;
+  const uint32_t NP = ps.np, NG = ps.chunks;
+  const uint32_t per = (NG + kScanGroups - 1) / kScanGroups;
+  const uint32_t g0 = sg * per < NG ? sg * per : NG;
+  const uint32_t g1 = g0 + per < NG ? g0 + per : NG;
+  const bool live = p < NP;
+  gptr<uint32_t> col = G(ps.hist) + p;
+  uint32_t sum = 0;
+  if (live) {
+#pragma unroll 8
+    for (uint32_t g = g0; g < g1; g++) sum += col[(uint64_t)g * NP];
+  }
+  s_part[sg][c] = sum;
+  __syncthreads();
+  if (sg == 0 && live) {
+    uint32_t tot = 0;
+    for (uint32_t q = 0; q < kScanGroups; q++) tot += s_part[q][c];
+    const uint32_t base =
+        tot <= ps.cap ? p * ps.cap : NP * ps.cap + atomicAdd(ps.spill_top, tot);
+    ps.pinfo[2 * p] = base;
+    ps.pinfo[2 * p + 1] = tot;
+    s_base[c] = base;
+  }
+  __syncthreads();
+  if (live) {
+    uint32_t off = s_base[c];
+    for (uint32_t q = 0; q < sg; q++) off += s_part[q][c];
+#pragma unroll 8
+    for (uint32_t g = g0; g < g1; g++) {
+      const uint32_t v = col[(uint64_t)g * NP];
+      col[(uint64_t)g * NP] = off;
+      off += v;
+    }
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void k_pscatter(TableView t,
+                                                     const uint64_t* __restrict__ keys,
+                                                     uint64_t n, PartScratch ps) {
+  extern __shared__ uint32_t s_o[];
+  const uint32_t NP = ps.np;
+  const uint32_t* H = ps.hist + (uint64_t)blockIdx.x * NP;
+  for (uint32_t q = threadIdx.x; q < NP; q += kBlock) s_o[q] = H[q];
+  __syncthreads();
+  const uint64_t i0 = (uint64_t)blockIdx.x * kPartChunk;
+  gptr<u64x2> ent = G(reinterpret_cast<u64x2*>(ps.ent));
+  for (uint32_t j = threadIdx.x; j < kPartChunk; j += kBlock) {
+    const uint64_t i = i0 + j;
+    if (i < n) {
+      const uint64_t k = keys[i];
+      if (!is_reserved(k)) {
+        const uint32_t pos = atomicAdd(&s_o[bucket_of(t, k) / kPartBuckets], 1u);
+        u64x2 v;
+        v.x = k;
+        v.y = i;
+        ent[pos] = v;
+      }
+    }
+  }
+}
+
+// Row tasks recorded by the lane pass, one word per batch index (0 = none),
+// executed in batch order by k_rowcopy.  The top two bits give the kind:
+//   kTaskIn:  input row i -> the table row at the address in the low bits
+//   kTaskOut: the table row at the address -> output row i
+//   kTaskFwd: output row j (low bits) -> output row i  (find_or_insert hit on
+//             a row that key j inserted earlier in the same batch)
+constexpr uint64_t kTaskIn = 1ull << 62;
+constexpr uint64_t kTaskOut = 2ull << 62;
+constexpr uint64_t kTaskFwd = 3ull << 62;
+constexpr uint64_t kTaskMask = (1ull << 62) - 1;
+constexpr uint8_t kNoSlot = 0xFF;
+
+// Executes and clears the row tasks of batch indices `i`, one per lane (a
+// lane with valid == false takes part without a task); the wave copies the
+// rows cooperatively.  `s_rows` is 64 words of LDS owned by the wave.
+template <int U>
+__device__ __forceinline__ void wave_run_tasks(const ApplyArgs& a, gptr<uint64_t> trow,
+                                               uint64_t i, bool valid, uint32_t row_bytes,
+                                               uint32_t* s_rows) {
+  using T = typename UnitT<U>::T;
+  const uint32_t lane = threadIdx.x & 63;
+  const uint64_t R = row_bytes;
+  uint64_t tv = 0;
+  if (valid) {
+    tv = trow[i];
+    if (tv) trow[i] = 0;
+  }
+  uint64_t src = 0, dst = 0;
+  if (tv) {
+    const uint64_t kind = tv & ~kTaskMask, val = tv & kTaskMask;
+    if (kind == kTaskIn) {
+      src = (uint64_t)(uintptr_t)(a.in_values + i * R);
+      dst = val;
+    } else if (kind == kTaskOut) {
+      src = val;
+      dst = (uint64_t)(uintptr_t)(a.io_values + i * R);
+    } else {
+      src = (uint64_t)(uintptr_t)(a.io_values + val * R);
+      dst = (uint64_t)(uintptr_t)(a.io_values + i * R);
+    }
+  }
+  const uint64_t hm = __ballot(tv != 0);
+  if (tv) s_rows[__popcll(hm & ((1ull << lane) - 1))] = lane;
+  __builtin_amdgcn_wave_barrier();
+  const uint32_t rows = __popcll(hm);
+  const uint32_t units = row_bytes / U;
+  uint32_t lpr = 64;
+  while (lpr > 1 && lpr / 2 >= units) lpr >>= 1;  // lanes per row
+  const uint32_t rpi = 64 / lpr;
+  const uint32_t sub = lane % lpr;
+  for (uint32_t r0 = 0; r0 < rows; r0 += 4 * rpi) {
+    const uint32_t r = r0 + lane / lpr;
+    const bool ok0 = r < rows, ok1 = r + rpi < rows, ok2 = r + 2 * rpi < rows,
+               ok3 = r + 3 * rpi < rows;
+    const uint32_t l0 = s_rows[ok0 ? r : 0], l1 = s_rows[ok1 ? r + rpi : 0],
+                   l2 = s_rows[ok2 ? r + 2 * rpi : 0], l3 = s_rows[ok3 ? r + 3 * rpi : 0];
+    gptr<const T> s0 = G<const T>((uintptr_t)shfl_u64(src, (int)l0, 64));
+    gptr<const T> s1 = G<const T>((uintptr_t)shfl_u64(src, (int)l1, 64));
+    gptr<const T> s2 = G<const T>((uintptr_t)shfl_u64(src, (int)l2, 64));
+    gptr<const T> s3 = G<const T>((uintptr_t)shfl_u64(src, (int)l3, 64));
+    gptr<T> d0 = G<T>((uintptr_t)shfl_u64(dst, (int)l0, 64));
+    gptr<T> d1 = G<T>((uintptr_t)shfl_u64(dst, (int)l1, 64));
+    gptr<T> d2 = G<T>((uintptr_t)shfl_u64(dst, (int)l2, 64));
+    gptr<T> d3 = G<T>((uintptr_t)shfl_u64(dst, (int)l3, 64));
+    for (uint32_t u = sub; u < units; u += lpr) {
+      const T v0 = s0[u], v1 = s1[u], v2 = s2[u], v3 = s3[u];
+      if (ok0) d0[u] = v0;
+      if (ok1) d1[u] = v1;
+      if (ok2) d2[u] = v2;
+      if (ok3) d3[u] = v3;
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+}
+
+template <int OP, int U>
+__global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a, PartScratch ps,
+                                                         int all) {
+  // accum_or_assign accumulates in place, in batch order, inside this kernel;
+  // the other operations record their row movements for k_rowcopy.
+  constexpr bool kDeferRows = OP != OP_ACCUM_OR_ASSIGN;
+  constexpr uint32_t kQ = kDeferRows ? 1 : kPartTaskCap;
+  __shared__ uint64_t s_key[kPartLds];
+  __shared__ uint32_t s_idx[kPartLds];
+  __shared__ uint8_t s_slot[kPartLds];  // slot whose row the step wrote
+  __shared__ uint32_t s_cnt[kPartBuckets], s_off[kPartBuckets], s_fill[kPartBuckets];
+  __shared__ uint32_t s_defer[kPartBuckets];
+  __shared__ uint32_t s_perm[kPartBuckets];  // buckets by decreasing key count
+  __shared__ uint32_t s_cls[64];             // buckets per key count class
+  __shared__ uint32_t s_rows[kBlock / 64][64];
+  __shared__ uint32_t s_dg[kPartBuckets * kDgStride];  // digest rows of the buckets
+  __shared__ uint32_t s_wsum[kBlock / 64];
+  __shared__ uint64_t s_src[kBlock / 64][kQ];
+  __shared__ uint64_t s_dst[kBlock / 64][kQ];
+  __shared__ uint32_t s_ndefer, s_c1, s_g;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const uint32_t p = blockIdx.x;
+  const uint32_t NP = ps.np, NG = ps.chunks;
+  if (!all && ps.pflag[p]) return;  // applied by k_apply_fast
+  const uint32_t base_e = ps.pinfo[2 * p], m = ps.pinfo[2 * p + 1];
+  const uint32_t B = t.B;
+  const uint64_t part_b0 = (uint64_t)p * kPartBuckets;
+  const uint32_t R = t.row_bytes;
+  const bool has_in = a.in_scores != nullptr;
+  gptr<const u64x2> ent = G(reinterpret_cast<const u64x2*>(ps.ent));
+  gptr<uint64_t> trow = G(ps.trow);
+  uint32_t added = 0;
+  if (tid == 0) s_g = 0;
+  uint32_t c0 = base_e;
+  const uint32_t end_e = base_e + m;
+  while (c0 < end_e) {
+    // This run of entries: the whole partition when it fits, else whole
+    // segments in chunk order.
+    if (tid == 0) {
+      uint32_t c1 = end_e;
+      if (m > kPartLds) {
+        uint32_t g = s_g;
+        c1 = c0;
+        while (g < NG) {
+          const uint32_t e = g + 1 < NG ? ps.hist[(uint64_t)(g + 1) * NP + p] : end_e;
+          if (e - c0 > kPartLds) break;
+          c1 = e;
+          g++;
+        }
+        s_g = g;
+      }
+      s_c1 = c1;
+      s_ndefer = 0;
+    }
+    s_cnt[tid] = 0;
+    if (tid < 64) s_cls[tid] = 0;
+    __syncthreads();
+    const uint32_t c1 = s_c1;
+    const uint32_t mc = c1 - c0;
+    // Group the run's entries by bucket.
+    for (uint32_t e = tid; e < mc; e += kBlock)
+      atomicAdd(&s_cnt[bucket_of(t, ent[c0 + e].x) % kPartBuckets], 1u);
+    __syncthreads();
+    {
+      const uint32_t v = s_cnt[tid];
+      uint32_t x = v;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t y = __shfl_up(x, d, 64);
+        if (lane >= (uint32_t)d) x += y;
+      }
+      if (lane == 63) s_wsum[wv] = x;
+      __syncthreads();
+      uint32_t pre = 0;
+      for (uint32_t q = 0; q < wv; q++) pre += s_wsum[q];
+      s_off[tid] = pre + x - v;
+      s_fill[tid] = pre + x - v;
+    }
+    __syncthreads();
+    for (uint32_t e = tid; e < mc; e += kBlock) {
+      const u64x2 v = ent[c0 + e];
+      const uint32_t pos = atomicAdd(&s_fill[bucket_of(t, v.x) % kPartBuckets], 1u);
+      s_key[pos] = v.x;
+      s_idx[pos] = (uint32_t)v.y;
+    }
+    if (kDeferRows) {
+      // Digest rows of the partition's buckets (one contiguous region).
+      gptr<const u32x4> dsrc = (gptr<const u32x4>)(G(t.digests) + part_b0 * B);
+      const uint32_t nbk =
+          t.buckets - part_b0 < kPartBuckets ? (uint32_t)(t.buckets - part_b0) : kPartBuckets;
+      for (uint32_t q = tid; q < nbk * 8; q += kBlock) {
+        const u32x4 v = dsrc[q];
+        uint32_t* row = s_dg + (q >> 3) * kDgStride + (q & 7) * 4;
+        row[0] = v.x;
+        row[1] = v.y;
+        row[2] = v.z;
+        row[3] = v.w;
+      }
+    }
+    __syncthreads();
+    if (kDeferRows) {
+      // Lanes take buckets in decreasing order of key count, so that a wave
+      // holds buckets of similar work (counts above 63 tie).
+      const uint32_t cc = s_cnt[tid] < 63 ? s_cnt[tid] : 63;
+      const uint32_t r = atomicAdd(&s_cls[63 - cc], 1u);
+      __syncthreads();
+      // Exclusive prefix of the 64 count classes, by one wave.
+      if (wv == 0) {
+        const uint32_t v = s_cls[lane];
+        uint32_t x = v;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+          const uint32_t y = __shfl_up(x, d, 64);
+          if (lane >= (uint32_t)d) x += y;
+        }
+        s_defer[lane] = x - v;  // class offsets (s_defer is free here)
+      }
+      __syncthreads();
+      s_perm[s_defer[63 - cc] + r] = tid;
+      __syncthreads();
+    }
+
+    // Lane pass: the lane owns bucket bk of the partition.
+    const uint32_t bk = kDeferRows ? s_perm[tid] : tid;
+    const uint64_t b = part_b0 + bk;
+    const bool own = b < t.buckets;
+    const uint32_t c = own ? s_cnt[bk] : 0;
+    const uint32_t o = s_off[bk];
+    const bool lane_ok = c > 0 && c <= kLaneMax;
+    if (lane_ok) {
+      // Batch order within the bucket (insertion sort of a short run).
+      for (uint32_t x = 1; x < c; x++) {
+        const uint64_t kx = s_key[o + x];
+        const uint32_t ix = s_idx[o + x];
+        uint32_t y = x;
+        while (y > 0 && s_idx[o + y - 1] > ix) {
+          s_key[o + y] = s_key[o + y - 1];
+          s_idx[o + y] = s_idx[o + y - 1];
+          y--;
+        }
+        s_key[o + y] = kx;
+        s_idx[o + y] = ix;
+      }
+    } else if (c > kLaneMax) {
+      s_defer[atomicAdd(&s_ndefer, 1u)] = bk << 16;
+    }
+    const uint64_t base = b * (uint64_t)B;
+    int32_t bsz = lane_ok ? G(t.bsize)[b] : 0;
+    const int32_t bsz0 = bsz;
+    uint32_t wr0 = 0, wr1 = 0, wr2 = 0, wr3 = 0;
+    if constexpr (kDeferRows) {
+      if (lane_ok) {
+        uint32_t* dg = s_dg + bk * kDgStride;
+        const gptr<uint8_t> rows0 = row_ptr(t, b, 0);
+        constexpr bool may_insert = OP != OP_ASSIGN_SCORES;
+        for (uint32_t step = 0; step < c; step++) {
+          const uint64_t k = s_key[o + step];
+          const uint64_t i = s_idx[o + step];
+          const uint64_t in = has_in ? G(a.in_scores)[i] : 0;
+          const uint64_t h = murmur3(k);
+          const uint32_t start = (uint32_t)(global_idx(t, h) & (B - 1));
+          const uint32_t d = key_digest(h);
+          int dup = 0;
+          const int slot =
+              probe_upsert_lds(t, dg, base, start, d, k, may_insert && bsz < (int32_t)B, &dup);
+          if (slot < 0 && may_insert) {
+            // Eviction path: the 16-lane pass resumes here, after running the
+            // row tasks recorded so far for this bucket.
+            s_defer[atomicAdd(&s_ndefer, 1u)] = (bk << 16) | step;
+            break;
+          }
+          uint64_t src = 0, dst = 0;
+          uint32_t res = 0;
+          if (slot >= 0) {
+            res = lane_apply<OP>(t, a, base, rows0, slot, dup, i, k, in, has_in, d, bsz, src,
+                                 dst);
+            if (res & kLaneDigest) reinterpret_cast<uint8_t*>(dg)[slot] = (uint8_t)d;
+          }
+          uint64_t task = 0;
+          uint8_t wrote = kNoSlot;
+          if (dst) {
+            const uint32_t sl = (uint32_t)slot;
+            const uint32_t bit = 1u << (sl & 31), wq = sl >> 5;
+            const uint32_t cur = wq == 0 ? wr0 : wq == 1 ? wr1 : wq == 2 ? wr2 : wr3;
+            // Latest earlier step of this bucket that wrote the row of `slot`.
+            uint32_t prev = kNone;
+            if (cur & bit)
+              for (uint32_t x = 0; x < step; x++)
+                if (s_slot[o + x] == (uint8_t)sl) prev = x;
+            if (res & kLaneRead) {
+              // A hit: read the row, or the input of the key that wrote it.
+              task = prev != kNone ? (kTaskFwd | s_idx[o + prev])
+                                   : (kTaskOut | (src & kTaskMask));
+            } else {
+              // The row is written: a later write of the same row supersedes.
+              if (prev != kNone) {
+                trow[s_idx[o + prev]] = 0;
+                s_slot[o + prev] = kNoSlot;
+              }
+              task = kTaskIn | (dst & kTaskMask);
+              wrote = (uint8_t)sl;
+              wr0 |= wq == 0 ? bit : 0u;
+              wr1 |= wq == 1 ? bit : 0u;
+              wr2 |= wq == 2 ? bit : 0u;
+              wr3 |= wq == 3 ? bit : 0u;
+            }
+          }
+          s_slot[o + step] = wrote;
+          if (task) trow[i] = task;
+        }
+      }
+    } else {
+      uint32_t maxc = lane_ok ? c : 0;
+#pragma unroll
+      for (int d = 32; d > 0; d >>= 1) {
+        const uint32_t y = __shfl_xor(maxc, d, 64);
+        maxc = y > maxc ? y : maxc;
+      }
+      bool active = lane_ok;
+      for (uint32_t step = 0; step < maxc; step++) {
+        uint64_t src = 0, dst = 0;
+        if (active && step < c) {
+          const uint64_t k = s_key[o + step];
+          const uint64_t i = s_idx[o + step];
+          const uint64_t in = has_in ? G(a.in_scores)[i] : 0;
+          int slot = -1;
+          if (!lane_step<OP>(t, a, b, base, i, k, in, has_in, bsz, src, dst, slot)) {
+            active = false;
+            s_defer[atomicAdd(&s_ndefer, 1u)] = (bk << 16) | step;
+          }
+        }
+        // Accumulations run in batch order: each step's tasks are executed
+        // before the next step reads rows.
+        const uint64_t tm = __ballot(dst != 0);
+        if (dst) {
+          const uint32_t r = __popcll(tm & ((1ull << lane) - 1));
+          s_src[wv][r] = src;
+          s_dst[wv][r] = dst;
+        }
+        __builtin_amdgcn_wave_barrier();
+        if (tm) flush_tasks<U, 2>(__popcll(tm), s_src[wv], s_dst[wv], R, a.value_type);
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+      }
+    }
+    if (lane_ok && bsz != bsz0) G(t.bsize)[b] = bsz;
+    added += (uint32_t)(bsz - bsz0);
+    __syncthreads();
+
+    // 16-lane pass over the buckets handed over: 16 groups per block.
+    const uint32_t nd = s_ndefer;
+    const uint32_t gl = tid & 15;
+    for (uint32_t q = tid >> 4; q < nd; q += kBlock / 16) {
+      const uint32_t v = s_defer[q];
+      const uint32_t l2 = v >> 16, st = v & 0xFFFFu;
+      const uint32_t c2 = s_cnt[l2], o2 = s_off[l2];
+      const uint64_t b2 = part_b0 + l2;
+      if constexpr (kDeferRows) {
+        // Row tasks the lane pass recorded for this bucket, in batch order.
+        for (uint32_t x = 0; x < st; x++) {
+          const uint64_t i = s_idx[o2 + x];
+          const uint64_t tv = trow[i];
+          if (tv == 0) continue;
+          const uint64_t kind = tv & ~kTaskMask, val = tv & kTaskMask;
+          gptr<const uint8_t> src;
+          gptr<uint8_t> dst;
+          if (kind == kTaskIn) {
+            src = G(a.in_values) + i * (uint64_t)R;
+            dst = G<uint8_t>((uintptr_t)val);
+          } else if (kind == kTaskOut) {
+            src = G<const uint8_t>((uintptr_t)val);
+            dst = G(a.io_values) + i * (uint64_t)R;
+          } else {
+            src = G(a.io_values) + val * (uint64_t)R;
+            dst = G(a.io_values) + i * (uint64_t)R;
+          }
+          copy_units<U>(dst, src, R, gl, 16);
+          if (gl == 0) trow[i] = 0;
+        }
+      }
+      Bucket16 S;
+      bucket_load(t, S, b2, gl);
+      if (c2 <= kLaneMax) {
+        for (uint32_t step = st; step < c2; step++)
+          apply_key<OP, U>(t, S, a, s_idx[o2 + step], s_key[o2 + step]);
+      } else {
+        // Long run, not sorted: take the entries by increasing batch index.
+        uint32_t last = 0;  // batch index + 1 of the previous key
+        for (uint32_t step = 0; step < c2; step++) {
+          uint32_t mi = kNone, mp = 0;
+          for (uint32_t x = gl; x < c2; x += 16) {
+            const uint32_t iv = s_idx[o2 + x] + 1u;
+            if (iv > last && iv < mi) {
+              mi = iv;
+              mp = x;
+            }
+          }
+#pragma unroll
+          for (int d = 8; d > 0; d >>= 1) {
+            const uint32_t om = __shfl_xor(mi, d, 16);
+            const uint32_t op = __shfl_xor(mp, d, 16);
+            if (om < mi) {
+              mi = om;
+              mp = op;
+            }
+          }
+          last = mi;
+          apply_key<OP, U>(t, S, a, (uint64_t)(mi - 1), s_key[o2 + mp]);
+        }
+      }
+      bucket_finish(t, S);
+    }
+    __syncthreads();
+    if (kDeferRows && c1 < end_e) {
+      // Another run follows: its keys may touch the same slots, so the row
+      // tasks of this run are executed now, in this block.
+      for (uint32_t e0 = 0; e0 < mc; e0 += kBlock) {
+        const uint32_t e = e0 + tid;
+        wave_run_tasks<U>(a, trow, e < mc ? s_idx[e] : 0, e < mc, R, s_rows[wv]);
+      }
+      __syncthreads();
+    }
+    c0 = c1;
+  }
+#pragma unroll
+  for (int d = 32; d > 0; d >>= 1) added += __shfl_xor(added, d, 64);
+  if (lane == 0 && added) atomicAdd(t.live, (unsigned long long)added);
+}
+
+// Single-run apply of a partition whose entries fit one LDS load and whose
+// buckets receive at most kLaneMax keys each (every partition, for uniform
+// keys); other partitions are left to k_apply_part (pflag[p] = 0).  One lane
+// per bucket applies the bucket's keys in batch order while no eviction is
+// needed and records row tasks; a bucket that needs the eviction path is
+// handed, with all its keys, to k_apply_deferred.  The lane's bucket state
+// (digest line, size, row base) is loaded at kernel start, alongside the
+// entries, and barriers order LDS only.
+template <int OP>
+__global__ __launch_bounds__(kBlock) void k_apply_fast(TableView t, ApplyArgs a, PartScratch ps) {
+  static_assert(OP != OP_ACCUM_OR_ASSIGN, "accumulation runs in k_apply_part");
+  constexpr uint32_t kPer = kPartLds / kBlock;  // entries per thread
+  __shared__ uint64_t s_key[kPartLds];
+  __shared__ uint32_t s_idx[kPartLds];
+  __shared__ uint8_t s_slot[kPartLds];
+  __shared__ uint32_t s_cnt[kPartBuckets], s_off[kPartBuckets], s_fill[kPartBuckets];
+  __shared__ uint32_t s_wsum[kBlock / 64];
+  __shared__ uint32_t s_big;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const uint32_t p = blockIdx.x;
+  const uint32_t base_e = ps.pinfo[2 * p], m = ps.pinfo[2 * p + 1];
+  if (m > kPartLds) {
+    if (tid == 0) ps.pflag[p] = 0;
+    return;
+  }
+  const uint32_t B = t.B;
+  const uint32_t R = t.row_bytes;
+  const uint64_t b = (uint64_t)p * kPartBuckets + tid;
+  const bool own = b < t.buckets;
+  const uint64_t base = b * (uint64_t)B;
+  // This lane's bucket state, fetched while the entries load.
+  DLine L;
+  int32_t bsz = 0;
+  gptr<uint8_t> rows0 = nullptr;
+  if (own) {
+    dl_load(L, G(t.digests) + base);
+    bsz = G(t.bsize)[b];
+    rows0 = row_ptr(t, b, 0);
+  }
+  gptr<const u64x2> ent = G(reinterpret_cast<const u64x2*>(ps.ent)) + base_e;
+  u64x2 ev[kPer];
+  uint32_t lb[kPer];
+#pragma unroll
+  for (uint32_t q = 0; q < kPer; q++) {
+    const uint32_t e = tid + q * kBlock;
+    if (e < m) {
+      ev[q] = ent[e];
+      lb[q] = (uint32_t)(bucket_of(t, ev[q].x) % kPartBuckets);
+    }
+  }
+  s_cnt[tid] = 0;
+  if (tid == 0) s_big = 0;
+  lds_barrier();
+#pragma unroll
+  for (uint32_t q = 0; q < kPer; q++)
+    if (tid + q * kBlock < m) atomicAdd(&s_cnt[lb[q]], 1u);
+  lds_barrier();
+  const uint32_t c = s_cnt[tid];
+  {
+    uint32_t x = c;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const uint32_t y = __shfl_up(x, d, 64);
+      if (lane >= (uint32_t)d) x += y;
+    }
+    if (lane == 63) s_wsum[wv] = x;
+    if (c > kLaneMax) s_big = 1;
+    lds_barrier();
+    uint32_t pre = 0;
+    for (uint32_t q = 0; q < wv; q++) pre += s_wsum[q];
+    s_off[tid] = pre + x - c;
+    s_fill[tid] = pre + x - c;
+  }
+  lds_barrier();
+  if (s_big) {
+    if (tid == 0) ps.pflag[p] = 0;  // a long bucket: k_apply_part orders it
+    return;
+  }
+  if (tid == 0) ps.pflag[p] = 1;
+#pragma unroll
+  for (uint32_t q = 0; q < kPer; q++) {
+    if (tid + q * kBlock < m) {
+      const uint32_t pos = atomicAdd(&s_fill[lb[q]], 1u);
+      s_key[pos] = ev[q].x;
+      s_idx[pos] = (uint32_t)ev[q].y;
+    }
+  }
+  lds_barrier();
+
+  // Lane pass over bucket b: its c keys sit at s_key/s_idx[o, o + c).
+  const uint32_t o = s_off[tid];
+  for (uint32_t x = 1; x < c; x++) {  // batch order (insertion sort)
+    const uint64_t kx = s_key[o + x];
+    const uint32_t ix = s_idx[o + x];
+    uint32_t y = x;
+    while (y > 0 && s_idx[o + y - 1] > ix) {
+      s_key[o + y] = s_key[o + y - 1];
+      s_idx[o + y] = s_idx[o + y - 1];
+      y--;
+    }
+    s_key[o + y] = kx;
+    s_idx[o + y] = ix;
+  }
+  const int32_t bsz0 = bsz;
+  const bool has_in = a.in_scores != nullptr;
+  gptr<uint64_t> trow = G(ps.trow);
+  constexpr bool may_insert = OP != OP_ASSIGN_SCORES;
+  uint32_t wr0 = 0, wr1 = 0, wr2 = 0, wr3 = 0;
+  uint32_t stop = c;  // first key left to the 16-lane kernel
+  for (uint32_t step = 0; step < c; step++) {
+    const uint64_t k = s_key[o + step];
+    const uint64_t i = s_idx[o + step];
+    const uint64_t in = has_in ? G(a.in_scores)[i] : 0;
+    const uint64_t h = murmur3(k);
+    const uint32_t start = (uint32_t)(global_idx(t, h) & (B - 1));
+    const uint32_t d = key_digest(h);
+    int dup = 0;
+    const int slot =
+        probe_upsert_reg(t, L, base, start, d, k, may_insert && bsz < (int32_t)B, &dup);
+    if (slot < 0 && may_insert) {
+      stop = step;
+      break;
+    }
+    uint64_t src = 0, dst = 0;
+    uint32_t res = 0;
+    if (slot >= 0) {
+      res = lane_apply<OP>(t, a, base, rows0, slot, dup, i, k, in, has_in, d, bsz, src, dst);
+      if (res & kLaneDigest) dl_set(L, (uint32_t)slot, d);
+    }
+    uint64_t task = 0;
+    uint8_t wrote = kNoSlot;
+    if (dst) {
+      const uint32_t sl = (uint32_t)slot;
+      const uint32_t bit = 1u << (sl & 31), wq = sl >> 5;
+      const uint32_t cur = wq == 0 ? wr0 : wq == 1 ? wr1 : wq == 2 ? wr2 : wr3;
+      // Latest earlier step of this bucket that wrote the row of `slot`.
+      uint32_t prev = kNone;
+      if (cur & bit)
+        for (uint32_t x = 0; x < step; x++)
+          if (s_slot[o + x] == (uint8_t)sl) prev = x;
+      if (res & kLaneRead) {
+        // A hit: read the row, or the input of the key that wrote it.
+        task = prev != kNone ? (kTaskFwd | s_idx[o + prev]) : (kTaskOut | (src & kTaskMask));
+      } else {
+        // The row is written: a later write of the same row supersedes.
+        if (prev != kNone) {
+          trow[s_idx[o + prev]] = 0;
+          s_slot[o + prev] = kNoSlot;
+        }
+        task = kTaskIn | (dst & kTaskMask);
+        wrote = (uint8_t)sl;
+        wr0 |= wq == 0 ? bit : 0u;
+        wr1 |= wq == 1 ? bit : 0u;
+        wr2 |= wq == 2 ? bit : 0u;
+        wr3 |= wq == 3 ? bit : 0u;
+      }
+    }
+    s_slot[o + step] = wrote;
+    if (task) trow[i] = task;
+  }
+  if (bsz != bsz0) G(t.bsize)[b] = bsz;
+  uint32_t added = (uint32_t)(bsz - bsz0);
+#pragma unroll
+  for (int d = 32; d > 0; d >>= 1) added += __shfl_xor(added, d, 64);
+  if (lane == 0 && added) atomicAdd(t.live, (unsigned long long)added);
+
+  // Buckets left to the eviction path: a record {bucket, keys, first key
+  // left, pool offset} and all the bucket's keys in batch order.
+  const bool defer = stop < c;
+  const uint64_t dm = __ballot(defer);
+  if (dm) {
+    uint32_t x = defer ? c : 0;  // inclusive prefix of pool entries
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const uint32_t y = __shfl_up(x, d, 64);
+      if (lane >= (uint32_t)d) x += y;
+    }
+    uint32_t rbase = 0, pbase = 0;
+    if (lane == 63) {
+      rbase = atomicAdd(&ps.dctr[0], (uint32_t)__popcll(dm));
+      pbase = atomicAdd(&ps.dctr[1], x);
+    }
+    rbase = __shfl(rbase, 63, 64);
+    pbase = __shfl(pbase, 63, 64);
+    if (defer) {
+      const uint32_t r = rbase + __popcll(dm & ((1ull << lane) - 1));
+      const uint32_t po = pbase + x - c;
+      gptr<uint32_t> rec = G(ps.drec) + 4 * (uint64_t)r;
+      rec[0] = (uint32_t)b;
+      rec[1] = c;
+      rec[2] = stop;
+      rec[3] = po;
+      gptr<u64x2> pool = G(reinterpret_cast<u64x2*>(ps.dpool)) + po;
+      for (uint32_t q = 0; q < c; q++) {
+        u64x2 v;
+        v.x = s_key[o + q];
+        v.y = s_idx[o + q];
+        pool[q] = v;
+      }
+    }
+  }
+}
+
+// One 16-lane group per bucket handed over by k_apply_fast: first the row
+// tasks recorded for the keys the lane already applied, then the remaining
+// keys through the eviction path, in batch order.
+template <int OP, int U>
+__global__ __launch_bounds__(kBlock) void k_apply_deferred(TableView t, ApplyArgs a,
+                                                           PartScratch ps) {
+  const uint32_t nrec = *(volatile uint32_t*)ps.dctr;
+  const uint32_t gl = threadIdx.x & 15;
+  const uint64_t ngroups = (uint64_t)gridDim.x * (kBlock / 16);
+  const uint32_t R = t.row_bytes;
+  gptr<uint64_t> trow = G(ps.trow);
+  gptr<const u64x2> pool = G(reinterpret_cast<const u64x2*>(ps.dpool));
+  for (uint64_t r = ((uint64_t)blockIdx.x * kBlock + threadIdx.x) >> 4; r < nrec;
+       r += ngroups) {
+    gptr<const uint32_t> rec = G(ps.drec) + 4 * r;
+    const uint64_t b = rec[0];
+    const uint32_t c = rec[1], st = rec[2], po = rec[3];
+    for (uint32_t x = 0; x < st; x++) {
+      const uint64_t i = pool[po + x].y;
+      const uint64_t tv = trow[i];
+      if (tv == 0) continue;
+      const uint64_t kind = tv & ~kTaskMask, val = tv & kTaskMask;
+      gptr<const uint8_t> src;
+      gptr<uint8_t> dst;
+      if (kind == kTaskIn) {
+        src = G(a.in_values) + i * (uint64_t)R;
+        dst = G<uint8_t>((uintptr_t)val);
+      } else if (kind == kTaskOut) {
+        src = G<const uint8_t>((uintptr_t)val);
+        dst = G(a.io_values) + i * (uint64_t)R;
+      } else {
+        src = G(a.io_values) + val * (uint64_t)R;
+        dst = G(a.io_values) + i * (uint64_t)R;
+      }
+      copy_units<U>(dst, src, R, gl, 16);
+      if (gl == 0) trow[i] = 0;
+    }
+    Bucket16 S;
+    bucket_load(t, S, b, gl);
+    for (uint32_t step = st; step < c; step++) {
+      const u64x2 v = pool[po + step];
+      apply_key<OP, U>(t, S, a, v.y, v.x);
+    }
+    bucket_finish(t, S);
+  }
+}
+
+// Executes the row tasks k_apply_part left, one batch index per lane.
+template <int U>
+__global__ __launch_bounds__(kBlock) void k_rowcopy(ApplyArgs a, uint64_t* __restrict__ trow,
+                                                    uint32_t row_bytes) {
+  __shared__ uint32_t s_rows[kBlock / 64][64];
+  const uint32_t wv = threadIdx.x >> 6;
+  const uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
+  wave_run_tasks<U>(a, G(trow), i, i < a.n, row_bytes, s_rows[wv]);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -878,7 +1963,7 @@ __global__ __launch_bounds__(kBlock) void k_apply_heavy(TableView t, ApplyArgs a
 __global__ __launch_bounds__(kBlock) void k_export_count(TableView t, uint64_t offset, uint64_t n,
                                                          uint32_t* __restrict__ block_cnt) {
   const uint64_t s = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
-  const bool live = s < n && !is_reserved(t.keys[offset + s]);
+  const bool live = s < n && !is_reserved(slot_key(t, offset + s));
   const uint64_t m = __ballot(live);
   __shared__ uint32_t w[kBlock / 64];
   if ((threadIdx.x & 63) == 0) w[threadIdx.x >> 6] = __popcll(m);
@@ -928,7 +2013,7 @@ __global__ __launch_bounds__(kBlock) void k_export_write(TableView t, uint64_t o
   const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const uint64_t s = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
   uint64_t k = kEmptyKey;
-  if (s < n) k = t.keys[offset + s];
+  if (s < n) k = slot_key(t, offset + s);
   const bool live = s < n && !is_reserved(k);
   const uint64_t m = __ballot(live);
   if (lane == 0) w[wv] = __popcll(m);
@@ -936,13 +2021,13 @@ __global__ __launch_bounds__(kBlock) void k_export_write(TableView t, uint64_t o
   uint32_t wbase = block_off[blockIdx.x];
   for (uint32_t q = 0; q < wv; q++) wbase += w[q];
   const uint32_t r = __popcll(m & ((1ull << lane) - 1));
-  const uint8_t* src = nullptr;
+  gptr<const uint8_t> src = nullptr;
   if (live) {
     const uint64_t g = offset + s;
     const uint64_t b = g >> t.bshift;
     const uint32_t slot = (uint32_t)(g & (t.B - 1));
     out_keys[wbase + r] = k;
-    if (out_scores) out_scores[wbase + r] = t.scores[g];
+    if (out_scores) out_scores[wbase + r] = slot_score(t, g);
     src = row_ptr(t, b, slot);
     s_rows[wv][r] = lane;
   }
@@ -964,8 +2049,8 @@ __global__ __launch_bounds__(kBlock) void k_export_write(TableView t, uint64_t o
       const uint32_t srcl = ok ? s_rows[wv][rr] : lane;
       const uint64_t sp = shfl_u64((uint64_t)(uintptr_t)src, (int)srcl, 64);
       if (ok) {
-        const T* sr = reinterpret_cast<const T*>((uintptr_t)sp);
-        T* dr = reinterpret_cast<T*>(out_vals + (uint64_t)(wbase + rr) * t.row_bytes);
+        gptr<const T> sr = G<const T>((uintptr_t)sp);
+        gptr<T> dr = G(reinterpret_cast<T*>(out_vals + (uint64_t)(wbase + rr) * t.row_bytes));
         for (uint32_t u = sub; u < units; u += lpr) dr[u] = sr[u];
       }
     }
@@ -1004,8 +2089,8 @@ __global__ void k_fill_u32(uint32_t* p, uint32_t v, uint64_t n) {
     p[q] = v;
 }
 
-__device__ __forceinline__ void thread_copy(uint8_t* dst, const uint8_t* src, uint32_t bytes,
-                                            int unit) {
+__device__ __forceinline__ void thread_copy(gptr<uint8_t> dst, gptr<const uint8_t> src,
+                                            uint32_t bytes, int unit) {
   copy_row(dst, src, bytes, unit, 0, 1);
 }
 
@@ -1018,18 +2103,17 @@ __device__ void rehash_defrag(const TableView& t, uint64_t b, uint32_t remove_po
   uint32_t offset = 1;
   while (offset < B) {
     const uint32_t cur = (remove_pos + offset) % B;
-    const uint64_t ck = t.keys[base + cur];
+    const uint64_t ck = slot_key(t, base + cur);
     if (ck == kEmptyKey) break;
     const uint64_t h = murmur3(ck);
     const uint64_t sp = (h % old_cap) % B;
     if ((sp <= remove_pos && remove_pos < cur) || (cur < sp && sp <= remove_pos) ||
         (remove_pos < cur && cur < sp)) {
-      t.keys[base + remove_pos] = ck;
-      t.scores[base + remove_pos] = t.scores[base + cur];
-      t.digests[base + remove_pos] = (uint8_t)key_digest(h);
+      slot_store(t, base + remove_pos, ck, slot_score(t, base + cur));
+      G(t.digests)[base + remove_pos] = (uint8_t)key_digest(h);
       thread_copy(row_ptr(t, b, remove_pos), row_ptr(t, b, cur), t.row_bytes, unit);
-      t.keys[base + cur] = kEmptyKey;
-      t.digests[base + cur] = kEmptyDigest;
+      slot_key(t, base + cur) = kEmptyKey;
+      G(t.digests)[base + cur] = kEmptyDigest;
       remove_pos = cur;
       offset = 1;
     } else {
@@ -1049,12 +2133,12 @@ __global__ __launch_bounds__(kBlock) void k_rehash(TableView t, uint64_t old_nb,
   const uint64_t new_cap = t.capacity;
   uint32_t kp = 0;
   while (kp < B) {
-    const uint64_t ck = t.keys[base + kp];
+    const uint64_t ck = slot_key(t, base + kp);
     if (ck == kEmptyKey || ck == kReclaimKey) {
       kp++;
       continue;
     }
-    const uint64_t cs = t.scores[base + kp];
+    const uint64_t cs = slot_score(t, base + kp);
     const uint64_t h = murmur3(ck);
     const uint64_t ngi = h % new_cap;
     const uint64_t nbk = ngi / B;
@@ -1066,18 +2150,17 @@ __global__ __launch_bounds__(kBlock) void k_rehash(TableView t, uint64_t old_nb,
     const uint64_t nbase = nbk * B;
     for (uint32_t o = 0; o < B; o++) {
       const uint32_t cp = (nkp + o) % B;
-      if (t.keys[nbase + cp] == kEmptyKey) {
-        t.keys[nbase + cp] = ck;
-        t.scores[nbase + cp] = cs;
-        t.digests[nbase + cp] = (uint8_t)key_digest(h);
-        t.bsize[nbk]++;
+      if (slot_key(t, nbase + cp) == kEmptyKey) {
+        slot_store(t, nbase + cp, ck, cs);
+        G(t.digests)[nbase + cp] = (uint8_t)key_digest(h);
+        G(t.bsize)[nbk]++;
         thread_copy(row_ptr(t, nbk, cp), row_ptr(t, b, kp), t.row_bytes, unit);
         break;
       }
     }
-    t.keys[base + kp] = kEmptyKey;
-    t.digests[base + kp] = kEmptyDigest;
-    t.bsize[b]--;
+    slot_key(t, base + kp) = kEmptyKey;
+    G(t.digests)[base + kp] = kEmptyDigest;
+    G(t.bsize)[b]--;
     rehash_defrag(t, b, kp, old_nb * B, unit);
     kp = 0;
   }
@@ -1106,6 +2189,7 @@ void launch_clear(const TableView& t, hipStream_t s) {
   const uint64_t slots = t.buckets * t.B;
   hipLaunchKernelGGL(k_init_slots, dim3(grid_for(slots, kBlock * 4, 65536)), dim3(kBlock), 0,
                      s, t, (uint64_t)0, slots, (uint64_t)0, t.buckets, 0);
+  launch_fill_u64(reinterpret_cast<uint64_t*>(t.live), 0, 1, s);
 }
 
 void launch_fill_u64(uint64_t* p, uint64_t v, uint64_t n, hipStream_t s) {
@@ -1120,14 +2204,19 @@ template <bool MISSED>
 static void find_dispatch(const TableView& t, const uint64_t* keys, uint64_t n, uint8_t* values,
                           uint8_t* founds, uint64_t* scores, uint64_t* mk, int32_t* mi,
                           int32_t* ms, int unit, hipStream_t s) {
-  const dim3 g(grid_for(n, kBlock, 1ull << 31)), b(kBlock);
+  constexpr int BLK = MISSED ? 1024 : kBlock;
+  const dim3 g(grid_for(n, BLK, 1ull << 31)), b(BLK);
+#define HKV_FIND_U(UU)                                                                      \
+  hipLaunchKernelGGL((k_find<UU, MISSED, BLK>), g, b, 0, s, t, keys, n, values, founds, scores, \
+                     mk, mi, ms)
   switch (unit) {
-    case 16: hipLaunchKernelGGL((k_find<16, MISSED>), g, b, 0, s, t, keys, n, values, founds, scores, mk, mi, ms); break;
-    case 8: hipLaunchKernelGGL((k_find<8, MISSED>), g, b, 0, s, t, keys, n, values, founds, scores, mk, mi, ms); break;
-    case 4: hipLaunchKernelGGL((k_find<4, MISSED>), g, b, 0, s, t, keys, n, values, founds, scores, mk, mi, ms); break;
-    case 2: hipLaunchKernelGGL((k_find<2, MISSED>), g, b, 0, s, t, keys, n, values, founds, scores, mk, mi, ms); break;
-    default: hipLaunchKernelGGL((k_find<1, MISSED>), g, b, 0, s, t, keys, n, values, founds, scores, mk, mi, ms); break;
+    case 16: HKV_FIND_U(16); break;
+    case 8: HKV_FIND_U(8); break;
+    case 4: HKV_FIND_U(4); break;
+    case 2: HKV_FIND_U(2); break;
+    default: HKV_FIND_U(1); break;
   }
+#undef HKV_FIND_U
 }
 
 void launch_find(const TableView& t, const uint64_t* keys, uint64_t n, uint8_t* values,
@@ -1181,6 +2270,45 @@ void launch_apply(const TableView& t, int op, const ApplyArgs& a, RouteScratch& 
     case OP_INSERT_AND_EVICT: apply_op<OP_INSERT_AND_EVICT>(t, a, rs, parity, s); break;
     case OP_ACCUM_OR_ASSIGN: apply_op<OP_ACCUM_OR_ASSIGN>(t, a, rs, parity, s); break;
     default: apply_op<OP_ASSIGN_SCORES>(t, a, rs, parity, s); break;
+  }
+}
+
+template <int OP>
+static void apply_part_op(const TableView& t, const ApplyArgs& a, const PartScratch& ps,
+                          hipStream_t s) {
+  const size_t lds = (size_t)ps.np * sizeof(uint32_t);
+  hipLaunchKernelGGL(k_pcount, dim3(ps.chunks), dim3(kBlock), lds, s, t, a.keys, a.n, ps);
+  hipLaunchKernelGGL(k_pscan, dim3((ps.np + 15) / 16), dim3(1024), 0, s, ps);
+  hipLaunchKernelGGL(k_pscatter, dim3(ps.chunks), dim3(kBlock), lds, s, t, a.keys, a.n, ps);
+  const dim3 g(ps.np), b(kBlock);
+  constexpr bool fast = OP != OP_ACCUM_OR_ASSIGN;
+  const bool rows = OP != OP_ACCUM_OR_ASSIGN && OP != OP_ASSIGN_SCORES;
+  const dim3 gr(grid_for(a.n, kBlock, 1ull << 31));
+  const dim3 gd(grid_for(a.n * 16, kBlock, 4096));
+  if constexpr (fast) hipLaunchKernelGGL((k_apply_fast<fast ? OP : 0>), g, b, 0, s, t, a, ps);
+#define HKV_PART_U(UU)                                                                       \
+  if constexpr (fast)                                                                        \
+    hipLaunchKernelGGL((k_apply_deferred<fast ? OP : 0, UU>), gd, b, 0, s, t, a, ps);        \
+  hipLaunchKernelGGL((k_apply_part<OP, UU>), g, b, 0, s, t, a, ps, fast ? 0 : 1);            \
+  if (rows) hipLaunchKernelGGL((k_rowcopy<UU>), gr, b, 0, s, a, ps.trow, t.row_bytes)
+  switch (a.unit) {
+    case 16: HKV_PART_U(16); break;
+    case 8: HKV_PART_U(8); break;
+    case 4: HKV_PART_U(4); break;
+    case 2: HKV_PART_U(2); break;
+    default: HKV_PART_U(1); break;
+  }
+#undef HKV_PART_U
+}
+
+void launch_apply_part(const TableView& t, int op, const ApplyArgs& a, const PartScratch& ps,
+                       hipStream_t s) {
+  switch (op) {
+    case OP_INSERT_OR_ASSIGN: apply_part_op<OP_INSERT_OR_ASSIGN>(t, a, ps, s); break;
+    case OP_FIND_OR_INSERT: apply_part_op<OP_FIND_OR_INSERT>(t, a, ps, s); break;
+    case OP_INSERT_AND_EVICT: apply_part_op<OP_INSERT_AND_EVICT>(t, a, ps, s); break;
+    case OP_ACCUM_OR_ASSIGN: apply_part_op<OP_ACCUM_OR_ASSIGN>(t, a, ps, s); break;
+    default: apply_part_op<OP_ASSIGN_SCORES>(t, a, ps, s); break;
   }
 }
 

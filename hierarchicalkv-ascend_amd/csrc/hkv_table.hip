@@ -5,7 +5,9 @@
 
 #include <algorithm>
 #include <chrono>
+#include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <string>
@@ -88,9 +90,9 @@ struct hkv_table {
   uint64_t clock_value = 0;
 
   uint8_t* digests = nullptr;
-  uint64_t* keys = nullptr;
-  uint64_t* scores = nullptr;
+  uint64_t* slots = nullptr;  // {key, score} records, 16 bytes per slot
   int32_t* bsize = nullptr;
+  uint64_t* live = nullptr;   // live keys, maintained by the kernels
 
   uint64_t slice_shift = 0;  // buckets per slice = 1 << slice_shift
   uint64_t remaining_hbm = 0;
@@ -107,6 +109,23 @@ struct hkv_table {
   uint64_t heavy_cap = 0;
   uint32_t* ctrl = nullptr;
   int parity = 0;
+  // partitioned apply scratch
+  bool force_route = false;  // HKV_APPLY_PATH=route selects the route path
+  uint32_t* p_hist = nullptr;
+  uint64_t p_hist_cap = 0;
+  uint64_t* p_ent = nullptr;
+  uint64_t p_ent_cap = 0;  // entries
+  uint32_t* p_info = nullptr;
+  uint64_t p_info_cap = 0;
+  uint32_t* p_spill = nullptr;
+  uint64_t* p_trow = nullptr;  // zero between calls
+  uint64_t p_trow_cap = 0;
+  uint32_t* p_flag = nullptr;
+  uint64_t p_flag_cap = 0;
+  uint32_t* p_drec = nullptr;
+  uint64_t* p_dpool = nullptr;
+  uint64_t p_defer_cap = 0;
+  uint32_t* p_dctr = nullptr;
   // export scratch
   uint32_t* blk = nullptr;
   uint64_t blk_cap = 0;
@@ -117,9 +136,9 @@ struct hkv_table {
   TableView view() const {
     TableView v{};
     v.digests = digests;
-    v.keys = keys;
-    v.scores = scores;
+    v.slots = slots;
     v.bsize = bsize;
+    v.live = reinterpret_cast<unsigned long long*>(live);
     v.slices = d_slices;
     v.capacity = C;
     v.buckets = nb;
@@ -180,9 +199,9 @@ struct hkv_table {
 
   void free_all() {
     (void)hipFree(digests);
-    (void)hipFree(keys);
-    (void)hipFree(scores);
+    (void)hipFree(slots);
     (void)hipFree(bsize);
+    (void)hipFree(live);
     for (auto& s : slices) {
       if (s.hbm) (void)hipFree(s.dev_ptr);
       else (void)hipHostFree(s.host_ptr);
@@ -193,6 +212,15 @@ struct hkv_table {
     (void)hipFree(pend);
     (void)hipFree(heavy);
     (void)hipFree(ctrl);
+    (void)hipFree(p_hist);
+    (void)hipFree(p_ent);
+    (void)hipFree(p_info);
+    (void)hipFree(p_spill);
+    (void)hipFree(p_trow);
+    (void)hipFree(p_flag);
+    (void)hipFree(p_drec);
+    (void)hipFree(p_dpool);
+    (void)hipFree(p_dctr);
     (void)hipFree(blk);
     (void)hipFree(d_sum);
     if (h_sum) (void)hipHostFree(h_sum);
@@ -218,6 +246,59 @@ struct hkv_table {
       hip_check(hipMalloc(&heavy, hneed * sizeof(uint32_t)), "hipMalloc(heavy)");
       heavy_cap = hneed;
     }
+  }
+
+  // Scratch of the partitioned apply path for a batch of n keys.  Returns
+  // false when the table has more partitions than the path supports.
+  bool part_scratch(uint64_t n, PartScratch* ps, hipStream_t s) {
+    const uint64_t np = (nb + kPartBuckets - 1) / kPartBuckets;
+    if (force_route || np > kMaxPartitions || n >= (1ull << 32)) return false;
+    const uint64_t ng = (n + kPartChunk - 1) / kPartChunk;
+    // Fixed region per partition: the mean plus eight standard deviations;
+    // a partition that receives more goes to the spill area, which holds n.
+    const double mu = std::ceil((double)n / (double)np);
+    uint64_t cap = (uint64_t)(mu + 8.0 * std::sqrt(mu) + 64.0);
+    cap = (cap + 63) & ~63ull;
+    if (np * cap + n >= (1ull << 32)) cap = 64;
+    const uint64_t hist = ng * np, ent = np * cap + n, info = 2 * np;
+    if (hist > p_hist_cap) {
+      if (p_hist) hip_check(hipFree(p_hist), "hipFree");
+      hip_check(hipMalloc(&p_hist, hist * sizeof(uint32_t)), "hipMalloc(part hist)");
+      p_hist_cap = hist;
+    }
+    if (ent > p_ent_cap) {
+      if (p_ent) hip_check(hipFree(p_ent), "hipFree");
+      hip_check(hipMalloc(&p_ent, ent * 16), "hipMalloc(part entries)");
+      p_ent_cap = ent;
+    }
+    if (info > p_info_cap) {
+      if (p_info) hip_check(hipFree(p_info), "hipFree");
+      hip_check(hipMalloc(&p_info, info * sizeof(uint32_t)), "hipMalloc(part info)");
+      p_info_cap = info;
+    }
+    if (!p_spill) hip_check(hipMalloc(&p_spill, sizeof(uint32_t)), "hipMalloc(part spill)");
+    if (n > p_trow_cap) {
+      if (p_trow) hip_check(hipFree(p_trow), "hipFree");
+      hip_check(hipMalloc(&p_trow, n * sizeof(uint64_t)), "hipMalloc(part tasks)");
+      launch_fill_u64(p_trow, 0, n, s);
+      p_trow_cap = n;
+    }
+    if (np > p_flag_cap) {
+      if (p_flag) hip_check(hipFree(p_flag), "hipFree");
+      hip_check(hipMalloc(&p_flag, np * sizeof(uint32_t)), "hipMalloc(part flags)");
+      p_flag_cap = np;
+    }
+    if (n > p_defer_cap) {
+      if (p_drec) hip_check(hipFree(p_drec), "hipFree");
+      if (p_dpool) hip_check(hipFree(p_dpool), "hipFree");
+      hip_check(hipMalloc(&p_drec, n * 4 * sizeof(uint32_t)), "hipMalloc(defer records)");
+      hip_check(hipMalloc(&p_dpool, n * 16), "hipMalloc(defer pool)");
+      p_defer_cap = n;
+    }
+    if (!p_dctr) hip_check(hipMalloc(&p_dctr, 2 * sizeof(uint32_t)), "hipMalloc(defer counts)");
+    *ps = PartScratch{p_hist, p_ent,  p_info,  p_spill,      p_trow,       p_flag,
+                      p_drec, p_dpool, p_dctr, (uint32_t)np, (uint32_t)ng, (uint32_t)cap};
+    return true;
   }
 
   // Pending-list length: large enough that, with keys spread uniformly, a
@@ -251,28 +332,24 @@ struct hkv_table {
     // include/table.h:360-377 followed by the rehash kernel.
     const uint64_t old_nb = nb, old_C = C;
     uint8_t* nd = nullptr;
-    uint64_t *nk = nullptr, *ns = nullptr;
+    uint64_t* nsl = nullptr;
     int32_t* nbs = nullptr;
     uint32_t* ncnt = nullptr;
     hip_check(hipMalloc(&nd, 2 * old_C), "hipMalloc(digests)");
-    hip_check(hipMalloc(&nk, 2 * old_C * 8), "hipMalloc(keys)");
-    hip_check(hipMalloc(&ns, 2 * old_C * 8), "hipMalloc(scores)");
+    hip_check(hipMalloc(&nsl, 2 * old_C * 16), "hipMalloc(slots)");
     hip_check(hipMalloc(&nbs, 2 * old_nb * 4), "hipMalloc(bsize)");
     hip_check(hipMalloc(&ncnt, 2 * old_nb * 4), "hipMalloc(cnt)");
     hip_check(hipMemcpyAsync(nd, digests, old_C, hipMemcpyDeviceToDevice, s), "copy");
-    hip_check(hipMemcpyAsync(nk, keys, old_C * 8, hipMemcpyDeviceToDevice, s), "copy");
-    hip_check(hipMemcpyAsync(ns, scores, old_C * 8, hipMemcpyDeviceToDevice, s), "copy");
+    hip_check(hipMemcpyAsync(nsl, slots, old_C * 16, hipMemcpyDeviceToDevice, s), "copy");
     hip_check(hipMemcpyAsync(nbs, bsize, old_nb * 4, hipMemcpyDeviceToDevice, s), "copy");
     launch_fill_u32(ncnt, 0, 2 * old_nb, s);
     hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
     (void)hipFree(digests);
-    (void)hipFree(keys);
-    (void)hipFree(scores);
+    (void)hipFree(slots);
     (void)hipFree(bsize);
     (void)hipFree(cnt);
     digests = nd;
-    keys = nk;
-    scores = ns;
+    slots = nsl;
     bsize = nbs;
     cnt = ncnt;
     nb = 2 * old_nb;
@@ -385,11 +462,16 @@ int insert_like(hkv_table* t, int op, uint64_t n, const void* keys, const void* 
   a.rule = rule;
   a.unit = min_unit(t, {in_values, io_values, ev_values});
   a.value_type = t->value_type;
-  const uint32_t P = t->pick_P(n);
-  t->ensure_route_scratch(n, P);
-  RouteScratch rs{t->cnt, t->pend, t->heavy, t->ctrl, P};
-  launch_apply(t->view(), op, a, rs, t->parity, s);
-  t->parity ^= 1;
+  PartScratch ps{};
+  if (t->part_scratch(n, &ps, s)) {
+    launch_apply_part(t->view(), op, a, ps, s);
+  } else {
+    const uint32_t P = t->pick_P(n);
+    t->ensure_route_scratch(n, P);
+    RouteScratch rs{t->cnt, t->pend, t->heavy, t->ctrl, P};
+    launch_apply(t->view(), op, a, rs, t->parity, s);
+    t->parity ^= 1;
+  }
   hip_check(hipGetLastError(), "kernel launch");
   return HKV_OK;
 }
@@ -451,6 +533,8 @@ int hkv_create(const hkv_options* o, int key_type, int value_type, int strategy,
     t->strategy = strategy;
     t->B = o->max_bucket_size;
     t->row = o->dim * (uint64_t)value_size(value_type);
+    const char* path = std::getenv("HKV_APPLY_PATH");
+    t->force_route = path && std::strcmp(path, "route") == 0;
     try {
       if (o->device_id >= 0) {
         hip_check(hipSetDevice(o->device_id), "hipSetDevice");
@@ -485,9 +569,9 @@ int hkv_create(const hkv_options* o, int key_type, int value_type, int strategy,
         t->slice_shift = std::min<uint64_t>(sh, log2_ceil(t->nb));
       }
       hip_check(hipMalloc(&t->digests, t->C), "hipMalloc(digests)");
-      hip_check(hipMalloc(&t->keys, t->C * 8), "hipMalloc(keys)");
-      hip_check(hipMalloc(&t->scores, t->C * 8), "hipMalloc(scores)");
+      hip_check(hipMalloc(&t->slots, t->C * 16), "hipMalloc(slots)");
       hip_check(hipMalloc(&t->bsize, t->nb * 4), "hipMalloc(bsize)");
+      hip_check(hipMalloc(&t->live, sizeof(uint64_t)), "hipMalloc(live)");
       hip_check(hipMalloc(&t->cnt, t->nb * 4), "hipMalloc(cnt)");
       hip_check(hipMalloc(&t->ctrl, 32 * sizeof(uint32_t)), "hipMalloc(ctrl)");
       hip_check(hipMalloc(&t->d_sum, sizeof(uint64_t)), "hipMalloc(sum)");
@@ -497,6 +581,7 @@ int hkv_create(const hkv_options* o, int key_type, int value_type, int strategy,
       launch_init_slots(t->view(), 0, t->nb, 0);
       launch_fill_u32(t->cnt, 0, t->nb, 0);
       launch_fill_u32(t->ctrl, 0, 32, 0);
+      launch_fill_u64(t->live, 0, 1, 0);
       hip_check(hipGetLastError(), "init launch");
       hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
     } catch (...) {
@@ -722,6 +807,18 @@ int hkv_set_lru_clock(hkv_table* t, uint64_t clock, int enable) {
     need_table(t);
     t->clock_override = enable != 0;
     t->clock_value = clock;
+  });
+}
+
+int hkv_live_count(hkv_table* t, hkv_stream stream, uint64_t* out) {
+  return guarded([&] {
+    need_table(t);
+    if (!out) fail(HKV_ERR_INVALID, "null output");
+    hip_check(hipMemcpyAsync(t->h_sum, t->live, sizeof(uint64_t), hipMemcpyDeviceToHost,
+                             S(stream)),
+              "hipMemcpyAsync");
+    hip_check(hipStreamSynchronize(S(stream)), "hipStreamSynchronize");
+    *out = *t->h_sum;
   });
 }
 

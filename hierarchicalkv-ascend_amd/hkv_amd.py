@@ -116,6 +116,7 @@ _SIGS = {
     "hkv_is_pure_hbm_mode": [_vp],
     "hkv_last_error": [],
     "hkv_set_lru_clock": [_vp, _u64, _i32],
+    "hkv_live_count": [_vp, _vp, ctypes.POINTER(_u64)],
 }
 _RESTYPES = {"hkv_options_default": None, "hkv_capacity": _u64, "hkv_dim": _u64,
              "hkv_max_bucket_size": _u64, "hkv_bucket_count": _u64,
@@ -331,3 +332,9 @@ class HashTable:
     def set_lru_clock(self, clock, enable=True):
         """Fixes the Lru/EpochLru clock (no reference counterpart)."""
         _check(_LIB.hkv_set_lru_clock(self._h, clock, int(enable)))
+
+    def live_count(self, stream=0):
+        """Live-key count kept on the device (no reference counterpart)."""
+        out = _u64(0)
+        _check(_LIB.hkv_live_count(self._h, _stream(stream), ctypes.byref(out)))
+        return out.value

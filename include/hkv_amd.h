@@ -170,6 +170,11 @@ const char* hkv_last_error(void);
  * enable=0 returns to the host monotonic clock read once per call. */
 int hkv_set_lru_clock(hkv_table* t, uint64_t clock, int enable);
 
+/* Test hook with no reference counterpart: the live-key count the kernels
+ * maintain on the device (it selects the find probe order).  Synchronizes
+ * `stream`; equals hkv_size() after every completed call. */
+int hkv_live_count(hkv_table* t, hkv_stream stream, uint64_t* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -167,6 +167,7 @@ class Pair:
     def assert_same_state(self):
         assert self.g.capacity() == self.o.capacity()
         assert self.g.size() == self.o.size()
+        assert self.g.live_count() == self.o.size()
         (ok, ov, os_), (gk, gv, gs) = self.export()
         np.testing.assert_array_equal(gk, ok)
         np.testing.assert_array_equal(gs, os_)
