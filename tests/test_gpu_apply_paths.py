@@ -1,0 +1,141 @@
+"""GPU parity of each route through the partitioned apply pipeline.
+
+A mutating batch is applied per partition (256 consecutive buckets):
+  * the single-run kernel, one lane per bucket, when the partition's keys fit
+    one LDS load (1024) and no bucket receives more than 32 of them;
+  * the 16-lane kernel for buckets of that kernel that need eviction;
+  * the multi-run kernel otherwise (large or skewed partitions);
+  * row copies recorded per batch index and executed by a streaming kernel,
+    with a later write of a row cancelling an earlier one and a
+    find_or_insert hit on a row inserted earlier in the same batch reading
+    that key's input.
+Tables here have 512 or 1024 buckets so that batches of ~1000 keys take the
+single-run route; the other GPU tests mostly use one-partition tables.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from gpu_pair import Pair
+from helpers import murmur3_np, uniform_keys
+
+pytestmark = pytest.mark.gpu
+
+
+def rand_vals(rng, n, dim):
+    return rng.uniform(-1, 1, (n, dim)).astype(np.float32)
+
+
+def keys_in_buckets(rng, n, capacity, b0, b1, exclude=()):
+    """`n` distinct keys whose bucket lies in [b0, b1) (power-of-2 capacity)."""
+    got, seen = [], set(int(x) for x in exclude)
+    while len(got) < n:
+        c = rng.integers(0, 2**63, size=1 << 18, dtype=np.uint64)
+        b = (murmur3_np(c) & np.uint64(capacity - 1)) // np.uint64(128)
+        for x in c[(b >= np.uint64(b0)) & (b < np.uint64(b1))]:
+            if int(x) not in seen:
+                seen.add(int(x))
+                got.append(x)
+                if len(got) == n:
+                    break
+    return np.array(got, np.uint64)
+
+
+@pytest.mark.parametrize("strategy,same_clock", [(O.LRU, True), (O.LRU, False),
+                                                 (O.CUSTOMIZED, False)])
+def test_single_run_fill_past_full(strategy, same_clock):
+    """~2 keys per bucket per batch into a 512-bucket table, from empty to
+    well past full: lane pass, hand-over at the first eviction and the
+    16-lane kernel."""
+    rng = np.random.default_rng(301 + same_clock)
+    cap = 1 << 16
+    p = Pair(cap, dim=8, strategy=strategy)
+    for b in range(90):
+        ks = uniform_keys(rng, 1024)
+        sc = None if strategy == O.LRU else rng.integers(0, 1 << 40, 1024, dtype=np.uint64)
+        p.insert_or_assign(ks, rand_vals(rng, 1024, 8), sc,
+                           clock=500 if same_clock else 500 + b)
+        if b % 15 == 14 or b == 89:
+            p.assert_same_state()
+    assert p.g.load_factor() == 1.0
+
+
+@pytest.mark.parametrize("strategy", [O.CUSTOMIZED, O.LRU])
+def test_single_run_repeated_keys(strategy):
+    """Batches drawn with replacement (unique_key=false): a row written twice
+    in one batch keeps the later key's input."""
+    rng = np.random.default_rng(303)
+    cap = 1 << 16
+    p = Pair(cap, dim=4, strategy=strategy)
+    pool = uniform_keys(rng, 40000)
+    for b in range(30):
+        ks = rng.choice(pool, 1024)
+        sc = None if strategy == O.LRU else rng.integers(0, 100, 1024, dtype=np.uint64)
+        p.insert_or_assign(ks, rand_vals(rng, 1024, 4), sc, unique_key=False, clock=9 + b)
+        if b % 10 == 9:
+            p.assert_same_state()
+    p.assert_same_state()
+
+
+@pytest.mark.parametrize("unique", [True, False])
+def test_single_run_find_or_insert_reads_same_batch_rows(unique):
+    """find_or_insert with keys repeated in a batch: the later occurrences
+    return the row the first one inserted (copied from its input)."""
+    rng = np.random.default_rng(304)
+    cap = 1 << 16
+    p = Pair(cap, dim=8, strategy=O.CUSTOMIZED)
+    pool = uniform_keys(rng, 30000)
+    for b in range(40):
+        if unique:
+            ks = rng.choice(pool, 1024, replace=False)
+        else:
+            ks = rng.choice(pool, 1024)
+        sc = rng.integers(0, 1 << 20, ks.size, dtype=np.uint64)
+        ov, gv = p.find_or_insert(ks, rand_vals(rng, ks.size, 8), sc, unique_key=unique,
+                                  clock=3 + b)
+        np.testing.assert_array_equal(gv.view(np.uint8), ov.view(np.uint8))
+        if b % 10 == 9:
+            p.assert_same_state()
+
+
+def test_single_run_insert_and_evict_and_assign_scores():
+    rng = np.random.default_rng(305)
+    cap = 1 << 16
+    p = Pair(cap, dim=4, strategy=O.LFU)
+    pool = uniform_keys(rng, 120000)
+    for b in range(80):
+        ks = pool[1024 * b:1024 * (b + 1)] if b % 2 == 0 else rng.choice(pool[:1024 * b], 1024,
+                                                                          replace=False)
+        sc = rng.integers(0, 1 << 20, 1024, dtype=np.uint64)
+        (ok, ov, os_), (gk, gv, gs) = p.insert_and_evict(ks, rand_vals(rng, 1024, 4), sc,
+                                                         clock=b)
+        o1 = np.lexsort((os_, ok))
+        o2 = np.lexsort((gs, gk))
+        np.testing.assert_array_equal(gk[o2], ok[o1])
+        np.testing.assert_array_equal(gs[o2], os_[o1])
+        np.testing.assert_array_equal(gv[o2].view(np.uint8), ov[o1].view(np.uint8))
+        if b % 8 == 7:
+            p.assign_scores(rng.choice(pool[:1024 * (b + 1)], 1024, replace=False),
+                            rng.integers(0, 1 << 10, 1024, dtype=np.uint64))
+            p.assert_same_state()
+    p.assert_same_state()
+
+
+def test_mixed_routes_in_one_call():
+    """One batch whose partitions take all three routes: partition 0 has a
+    bucket with 40 keys, partition 2 receives 1100 keys, partitions 1 and 3
+    take the single-run kernel."""
+    rng = np.random.default_rng(306)
+    cap = 1 << 17  # 1024 buckets, 4 partitions
+    p = Pair(cap, dim=4, strategy=O.CUSTOMIZED)
+    for b in range(6):
+        heavy = keys_in_buckets(rng, 40, cap, 3, 4)
+        big = keys_in_buckets(rng, 1100, cap, 512, 768, exclude=heavy)
+        rest = np.concatenate([keys_in_buckets(rng, 300, cap, 256, 512),
+                               keys_in_buckets(rng, 300, cap, 768, 1024)])
+        ks = np.concatenate([heavy, big, rest])
+        rng.shuffle(ks)
+        p.insert_or_assign(ks, rand_vals(rng, ks.size, 4),
+                           rng.integers(0, 1 << 30, ks.size, dtype=np.uint64))
+        p.assert_same_state()
+        p.assert_same_find(ks)
