@@ -738,106 +738,6 @@ __device__ __forceinline__ int probe_upsert(const TableView& t, uint64_t base, u
   return -1;
 }
 
-// The digest line of one bucket (128 digests, slot s in byte s) held in
-// registers by the lane that owns the bucket, so that its probes read no
-// memory: the lane is the bucket's only writer and keeps the copy current.
-struct DLine {
-  u32x4 c0, c1, c2, c3, c4, c5, c6, c7;
-};
-
-__device__ __forceinline__ void dl_load(DLine& L, gptr<const uint8_t> dg) {
-  gptr<const u32x4> q = (gptr<const u32x4>)dg;
-  L.c0 = q[0];
-  L.c1 = q[1];
-  L.c2 = q[2];
-  L.c3 = q[3];
-  L.c4 = q[4];
-  L.c5 = q[5];
-  L.c6 = q[6];
-  L.c7 = q[7];
-}
-
-// Chunk c of the line.  Written as mask arithmetic rather than a chain of
-// selects, which the compiler would turn into an indexed stack array.
-__device__ __forceinline__ u32x4 dl_chunk(const DLine& L, uint32_t c) {
-  const uint32_t m0 = 0u - (c == 0), m1 = 0u - (c == 1), m2 = 0u - (c == 2),
-                 m3 = 0u - (c == 3), m4 = 0u - (c == 4), m5 = 0u - (c == 5),
-                 m6 = 0u - (c == 6), m7 = 0u - (c == 7);
-  return (L.c0 & m0) | (L.c1 & m1) | (L.c2 & m2) | (L.c3 & m3) | (L.c4 & m4) | (L.c5 & m5) |
-         (L.c6 & m6) | (L.c7 & m7);
-}
-
-// Digests of the 4-slot group starting at slot g (g % 4 == 0).
-__device__ __forceinline__ uint32_t dl_word(const DLine& L, uint32_t g) {
-  const u32x4 ch = dl_chunk(L, g >> 4);
-  const uint32_t wi = (g >> 2) & 3;
-  return wi == 0 ? ch.x : wi == 1 ? ch.y : wi == 2 ? ch.z : ch.w;
-}
-
-__device__ __forceinline__ void dl_set(DLine& L, uint32_t p, uint32_t d) {
-  const uint32_t c = p >> 4, wi = (p >> 2) & 3, sh = 8 * (p & 3);
-  const uint32_t keep = ~(0xFFu << sh), v = d << sh;
-  // Byte p of the line: clear it and or in d, in every chunk under a mask
-  // that is all ones only for chunk c and word wi.
-  u32x4 km, vm;
-  km.x = wi == 0 ? keep : ~0u;
-  km.y = wi == 1 ? keep : ~0u;
-  km.z = wi == 2 ? keep : ~0u;
-  km.w = wi == 3 ? keep : ~0u;
-  vm.x = wi == 0 ? v : 0u;
-  vm.y = wi == 1 ? v : 0u;
-  vm.z = wi == 2 ? v : 0u;
-  vm.w = wi == 3 ? v : 0u;
-#define HKV_DL_SET(CC, N)                   \
-  {                                         \
-    const uint32_t on = 0u - (c == N);      \
-    L.CC = (L.CC & (km | ~on)) | (vm & on); \
-  }
-  HKV_DL_SET(c0, 0)
-  HKV_DL_SET(c1, 1)
-  HKV_DL_SET(c2, 2)
-  HKV_DL_SET(c3, 3)
-  HKV_DL_SET(c4, 4)
-  HKV_DL_SET(c5, 5)
-  HKV_DL_SET(c6, 6)
-  HKV_DL_SET(c7, 7)
-#undef HKV_DL_SET
-}
-
-// probe_upsert on a register digest line.
-__device__ __forceinline__ int probe_upsert_reg(const TableView& t, const DLine& L,
-                                                uint64_t base, uint32_t start, uint32_t d,
-                                                uint64_t k, bool not_full, int* dup) {
-  const uint32_t B = t.B;
-  const uint32_t a = start & ~3u;
-  const uint32_t rep = d * 0x01010101u;
-  const uint32_t erep = (uint32_t)kEmptyDigest * 0x01010101u;
-  for (uint32_t off = 0; off < B + 4; off += 4) {
-    const uint32_t g = (a + off) & (B - 1);
-    const uint32_t w = dl_word(L, g);
-    uint32_t m = eq_bytes4(w, rep);
-    while (m) {
-      const uint32_t j = __builtin_ctz(m);
-      m &= m - 1;
-      if (slot_key(t, base + g + j) == k) {
-        *dup = 1;
-        return (int)(g + j);
-      }
-    }
-    if (!not_full) continue;
-    uint32_t e = eq_bytes4(w, erep);
-    while (e) {
-      const uint32_t j = __builtin_ctz(e);
-      e &= e - 1;
-      const uint32_t p = g + j;
-      if (off == 0 && p < start) continue;
-      *dup = 0;
-      return (int)p;
-    }
-  }
-  return -1;
-}
-
 // Workgroup barrier that orders LDS only (global stores stay in flight).
 __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
@@ -1301,37 +1201,16 @@ constexpr uint64_t kTaskFwd = 3ull << 62;
 constexpr uint64_t kTaskMask = (1ull << 62) - 1;
 constexpr uint8_t kNoSlot = 0xFF;
 
-// Executes and clears the row tasks of batch indices `i`, one per lane (a
-// lane with valid == false takes part without a task); the wave copies the
-// rows cooperatively.  `s_rows` is 64 words of LDS owned by the wave.
+// Copies one row per lane that has a task (dst != 0), from src to dst; the
+// wave copies the rows cooperatively, four rows per lane group in flight.
+// `s_rows` is 64 words of LDS owned by the wave.
 template <int U>
-__device__ __forceinline__ void wave_run_tasks(const ApplyArgs& a, gptr<uint64_t> trow,
-                                               uint64_t i, bool valid, uint32_t row_bytes,
-                                               uint32_t* s_rows) {
+__device__ __forceinline__ void wave_copy_pairs(uint64_t src, uint64_t dst, uint32_t row_bytes,
+                                                uint32_t* s_rows) {
   using T = typename UnitT<U>::T;
   const uint32_t lane = threadIdx.x & 63;
-  const uint64_t R = row_bytes;
-  uint64_t tv = 0;
-  if (valid) {
-    tv = trow[i];
-    if (tv) trow[i] = 0;
-  }
-  uint64_t src = 0, dst = 0;
-  if (tv) {
-    const uint64_t kind = tv & ~kTaskMask, val = tv & kTaskMask;
-    if (kind == kTaskIn) {
-      src = (uint64_t)(uintptr_t)(a.in_values + i * R);
-      dst = val;
-    } else if (kind == kTaskOut) {
-      src = val;
-      dst = (uint64_t)(uintptr_t)(a.io_values + i * R);
-    } else {
-      src = (uint64_t)(uintptr_t)(a.io_values + val * R);
-      dst = (uint64_t)(uintptr_t)(a.io_values + i * R);
-    }
-  }
-  const uint64_t hm = __ballot(tv != 0);
-  if (tv) s_rows[__popcll(hm & ((1ull << lane) - 1))] = lane;
+  const uint64_t hm = __ballot(dst != 0);
+  if (dst) s_rows[__popcll(hm & ((1ull << lane) - 1))] = lane;
   __builtin_amdgcn_wave_barrier();
   const uint32_t rows = __popcll(hm);
   const uint32_t units = row_bytes / U;
@@ -1362,6 +1241,76 @@ __device__ __forceinline__ void wave_run_tasks(const ApplyArgs& a, gptr<uint64_t
     }
   }
   __builtin_amdgcn_wave_barrier();
+}
+
+// wave_copy_pairs with Q rows per lane group in flight: all loads of a round
+// are issued before its first store, and rows past the end are not touched.
+template <int U, int Q>
+__device__ __forceinline__ void wave_copy_pairs_q(uint64_t src, uint64_t dst, uint32_t row_bytes,
+                                                  uint32_t* s_rows) {
+  using T = typename UnitT<U>::T;
+  const uint32_t lane = threadIdx.x & 63;
+  const uint64_t hm = __ballot(dst != 0);
+  if (dst) s_rows[__popcll(hm & ((1ull << lane) - 1))] = lane;
+  __builtin_amdgcn_wave_barrier();
+  const uint32_t rows = __popcll(hm);
+  const uint32_t units = row_bytes / U;
+  uint32_t lpr = 64;
+  while (lpr > 1 && lpr / 2 >= units) lpr >>= 1;  // lanes per row
+  const uint32_t rpi = 64 / lpr;
+  const uint32_t sub = lane % lpr;
+  for (uint32_t r0 = 0; r0 < rows; r0 += Q * rpi) {
+    gptr<const T> s[Q];
+    gptr<T> d[Q];
+    bool ok[Q];
+#pragma unroll
+    for (int q = 0; q < Q; q++) {
+      const uint32_t r = r0 + q * rpi + lane / lpr;
+      ok[q] = r < rows;
+      const uint32_t l = s_rows[ok[q] ? r : 0];
+      s[q] = G<const T>((uintptr_t)shfl_u64(src, (int)l, 64));
+      d[q] = G<T>((uintptr_t)shfl_u64(dst, (int)l, 64));
+    }
+    for (uint32_t u = sub; u < units; u += lpr) {
+      T v[Q];
+#pragma unroll
+      for (int q = 0; q < Q; q++)
+        if (ok[q]) v[q] = s[q][u];
+#pragma unroll
+      for (int q = 0; q < Q; q++)
+        if (ok[q]) d[q][u] = v[q];
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+}
+
+// Executes and clears the row tasks of batch indices `i`, one per lane (a
+// lane with valid == false takes part without a task).
+template <int U>
+__device__ __forceinline__ void wave_run_tasks(const ApplyArgs& a, gptr<uint64_t> trow,
+                                               uint64_t i, bool valid, uint32_t row_bytes,
+                                               uint32_t* s_rows) {
+  const uint64_t R = row_bytes;
+  uint64_t tv = 0;
+  if (valid) {
+    tv = trow[i];
+    if (tv) trow[i] = 0;
+  }
+  uint64_t src = 0, dst = 0;
+  if (tv) {
+    const uint64_t kind = tv & ~kTaskMask, val = tv & kTaskMask;
+    if (kind == kTaskIn) {
+      src = (uint64_t)(uintptr_t)(a.in_values + i * R);
+      dst = val;
+    } else if (kind == kTaskOut) {
+      src = val;
+      dst = (uint64_t)(uintptr_t)(a.io_values + i * R);
+    } else {
+      src = (uint64_t)(uintptr_t)(a.io_values + val * R);
+      dst = (uint64_t)(uintptr_t)(a.io_values + i * R);
+    }
+  }
+  wave_copy_pairs<U>(src, dst, row_bytes, s_rows);
 }
 
 template <int OP, int U>
@@ -1677,9 +1626,9 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
       bucket_finish(t, S);
     }
     __syncthreads();
-    if (kDeferRows && c1 < end_e) {
-      // Another run follows: its keys may touch the same slots, so the row
-      // tasks of this run are executed now, in this block.
+    if (kDeferRows) {
+      // The row tasks of this run, executed before another run can touch
+      // the same slots.
       for (uint32_t e0 = 0; e0 < mc; e0 += kBlock) {
         const uint32_t e = e0 + tid;
         wave_run_tasks<U>(a, trow, e < mc ? s_idx[e] : 0, e < mc, R, s_rows[wv]);
@@ -1693,65 +1642,229 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
   if (lane == 0 && added) atomicAdd(t.live, (unsigned long long)added);
 }
 
-// Single-run apply of a partition whose entries fit one LDS load and whose
-// buckets receive at most kLaneMax keys each (every partition, for uniform
-// keys); other partitions are left to k_apply_part (pflag[p] = 0).  One lane
-// per bucket applies the bucket's keys in batch order while no eviction is
-// needed and records row tasks; a bucket that needs the eviction path is
-// handed, with all its keys, to k_apply_deferred.  The lane's bucket state
-// (digest line, size, row base) is loaded at kernel start, alongside the
-// entries, and barriers order LDS only.
-template <int OP>
-__global__ __launch_bounds__(kBlock) void k_apply_fast(TableView t, ApplyArgs a, PartScratch ps) {
+// Single-run apply of a partition whose entries fit one LDS load (kFastLds)
+// and whose buckets receive at most kLaneMax keys each (every partition, for
+// uniform keys); other partitions are left to k_apply_part (pflag[p] = 0).
+//
+// The batch-order semantics (keys applied one at a time in increasing batch
+// index, each by the reference's per-key algorithm) are reproduced with the
+// keys processed in parallel, one thread per key:
+//  B. every key probes the table as it was before the call, over the two
+//     16-slot digest chunks from its start group: the key is present at a
+//     slot, or absent with a first EMPTY slot, or undecided;
+//  C. per bucket, the first key in batch order whose outcome could depend on
+//     earlier keys of the call: the same key met again, two absent keys with
+//     the same first EMPTY slot, an absent key that would find the bucket
+//     full, or an undecided probe.  Up to that key the parallel outcomes are
+//     the sequential ones: a probe ends at its first EMPTY slot, so an
+//     earlier key's new slot lies on a later key's probe only when both are
+//     that slot;
+//  S. the rest of such a bucket, by one lane in batch order, probing the
+//     digests in memory and the call's own insertions in LDS.  At a key that
+//     needs the eviction path the lane hands the rest of the bucket to
+//     k_apply_deferred;
+//  W. the metadata of every applied key (one record per slot), then the
+//     block copies the rows of all its tasks.
+// No global store precedes the last global load of a phase that waits on it
+// (gfx9 counts loads and stores on one in-order counter, so a load issued
+// after stores would wait for them).
+constexpr uint32_t kFastLds = 704;  // entries of a partition the fast pass takes
+
+// Per-entry flags of the fast pass: the metadata record (bits 0-1), the row
+// task (bits 2-3) and the outcome on the table before the call (bits 4-5).
+constexpr uint8_t kMetaKey = 1;     // new key: key and score written at the slot
+constexpr uint8_t kMetaScore = 2;   // present key: score written
+constexpr uint8_t kMetaMask = 3;
+constexpr uint8_t kTkIn = 1 << 2;   // input row -> table row
+constexpr uint8_t kTkOut = 2 << 2;  // table row -> output row
+constexpr uint8_t kTkFwd = 3 << 2;  // input row of the earlier key that wrote the slot -> output row
+constexpr uint8_t kTkMask = 3 << 2;
+constexpr uint8_t kResNew = 1 << 4;   // absent; the slot is the probe's first EMPTY slot
+constexpr uint8_t kResDup = 2 << 4;   // present at the slot
+constexpr uint8_t kResSlow = 3 << 4;  // undecided by the window (or needs the serial lane)
+constexpr uint8_t kResMask = 3 << 4;
+
+__device__ __forceinline__ uint32_t sel4(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3,
+                                         uint32_t q) {
+  return q == 0 ? w0 : q == 1 ? w1 : q == 2 ? w2 : w3;
+}
+
+// Probe of one key over the two 16-slot digest chunks w0 (the chunk of
+// start's group) and w1 (the next one, circularly), in the order of
+// find_without_lock / insert_or_assign_kernel.h:105-183: 4-slot groups from
+// start's group; in each group first the digest matches, then the EMPTY
+// slots (in the first group only at or after start).
+struct WinProbe {
+  uint32_t slot;    // first EMPTY slot of the probe (when found)
+  uint32_t c0, c1;  // first two digest matches met up to that group (kNone: none)
+  bool found;       // the probe reached an EMPTY slot inside the window
+  bool over;        // more than two digest matches
+};
+
+__device__ __forceinline__ WinProbe probe_window(u32x4 w0, u32x4 w1, uint32_t start, uint32_t d,
+                                                 uint32_t B) {
+  const uint32_t a = start & ~3u;
+  const uint32_t cbase = a & ~15u;    // first slot of chunk w0
+  const uint32_t g0 = (a >> 2) & 3u;  // start's group inside w0
+  const uint32_t rep = d * 0x01010101u;
+  const uint32_t erep = (uint32_t)kEmptyDigest * 0x01010101u;
+  const uint32_t first_mask = ~((1u << (start - a)) - 1u) & 0xFu;
+  const uint32_t words[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+  WinProbe r{0, kNone, kNone, false, false};
+#pragma unroll
+  for (uint32_t q = 0; q < 8; q++) {
+    if (q < g0 || r.found) continue;
+    const uint32_t gs = (cbase + 4 * q) & (B - 1);  // first slot of the group
+    uint32_t m = eq_bytes4(words[q], rep);
+    while (m) {
+      const uint32_t p = gs + __builtin_ctz(m);
+      m &= m - 1;
+      if (r.c0 == kNone) r.c0 = p;
+      else if (r.c1 == kNone) r.c1 = p;
+      else r.over = true;
+    }
+    uint32_t e = eq_bytes4(words[q], erep);
+    if (q == g0) e &= first_mask;
+    if (e) {
+      r.found = true;
+      r.slot = gs + __builtin_ctz(e);
+    }
+  }
+  return r;
+}
+
+// Entry x < hi of the bucket (entries [lo, hi)) with rank r.
+__device__ __forceinline__ uint32_t entry_of_rank(const uint8_t* s_rank, uint32_t lo, uint32_t hi,
+                                                  uint32_t r) {
+  uint32_t e = lo;
+  for (uint32_t x = lo; x < hi; x++)
+    if (s_rank[x] == r) e = x;
+  return e;
+}
+
+// Probe of key k for the serial lane, over the bucket's digests in memory.
+// Slots filled by the call's earlier keys (bit set in f0..f3) show the empty
+// digest in memory; their keys are those of the entries of rank < r whose
+// outcome took the slot.  Returns the slot holding k (*dup = 1), else the
+// first EMPTY slot when `empties` (*dup = 0), else -1.
+__device__ __forceinline__ int probe_serial(const TableView& t, uint64_t base, uint32_t f0,
+                                            uint32_t f1, uint32_t f2, uint32_t f3,
+                                            const uint64_t* s_key, const uint8_t* s_slot,
+                                            const uint8_t* s_fl, const uint8_t* s_rank,
+                                            uint32_t lo, uint32_t hi, uint32_t r, uint32_t start,
+                                            uint32_t d, uint64_t k, bool empties, int* dup) {
+  const uint32_t B = t.B;
+  gptr<const u32x4> drow = (gptr<const u32x4>)(G(t.digests) + base);
+  const uint32_t a = start & ~3u;
+  const uint32_t rep = d * 0x01010101u;
+  const uint32_t erep = (uint32_t)kEmptyDigest * 0x01010101u;
+  uint32_t cur = kNone;
+  u32x4 chunk = {0, 0, 0, 0};
+  for (uint32_t off = 0; off < B + 4; off += 4) {
+    const uint32_t g = (a + off) & (B - 1);
+    if ((g >> 4) != cur) {
+      cur = g >> 4;
+      chunk = drow[cur];
+    }
+    const uint32_t wi = (g >> 2) & 3;
+    const uint32_t w = wi == 0 ? chunk.x : wi == 1 ? chunk.y : wi == 2 ? chunk.z : chunk.w;
+    const uint32_t fm = (sel4(f0, f1, f2, f3, g >> 5) >> (g & 31)) & 0xFu;
+    uint32_t m = eq_bytes4(w, rep) & ~fm;
+    while (m) {
+      const uint32_t j = __builtin_ctz(m);
+      m &= m - 1;
+      if (slot_key(t, base + g + j) == k) {
+        *dup = 1;
+        return (int)(g + j);
+      }
+    }
+    uint32_t fq = fm;
+    while (fq) {
+      const uint32_t p = g + __builtin_ctz(fq);
+      fq &= fq - 1;
+      for (uint32_t x = lo; x < hi; x++)
+        if (s_rank[x] < r && s_slot[x] == p && (s_fl[x] & kResMask) == kResNew &&
+            s_key[x] == k) {
+          *dup = 1;
+          return (int)p;
+        }
+    }
+    if (!empties) continue;
+    uint32_t e = eq_bytes4(w, erep) & ~fm;
+    if (off == 0) e &= ~((1u << (start - a)) - 1u);
+    if (e) {
+      *dup = 0;
+      return (int)(g + __builtin_ctz(e));
+    }
+  }
+  return -1;
+}
+
+template <int OP, int U>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_apply_fast(TableView t, ApplyArgs a, PartScratch ps) {
   static_assert(OP != OP_ACCUM_OR_ASSIGN, "accumulation runs in k_apply_part");
-  constexpr uint32_t kPer = kPartLds / kBlock;  // entries per thread
-  __shared__ uint64_t s_key[kPartLds];
-  __shared__ uint32_t s_idx[kPartLds];
-  __shared__ uint8_t s_slot[kPartLds];
-  __shared__ uint32_t s_cnt[kPartBuckets], s_off[kPartBuckets], s_fill[kPartBuckets];
+  constexpr uint32_t kPer = (kFastLds + kBlock - 1) / kBlock;  // entries per thread
+  constexpr bool may_insert = OP != OP_ASSIGN_SCORES;
+  constexpr bool moves_rows = OP != OP_ASSIGN_SCORES;
+  constexpr bool reads_rows = OP == OP_FIND_OR_INSERT;
+  __shared__ uint64_t s_key[kFastLds];
+  __shared__ uint64_t s_sc[kFastLds];     // input score, then the score of the record
+  __shared__ uint32_t s_idx[kFastLds];    // batch index
+  __shared__ uint8_t s_slot[kFastLds];    // slot of the outcome (kNoSlot: none)
+  __shared__ uint8_t s_fl[kFastLds];      // outcome, metadata record and row task
+  __shared__ uint8_t s_rank[kFastLds];    // batch order inside the bucket
+  __shared__ uint32_t s_cnt[kPartBuckets];  // keys per bucket, fill pointers, then stops
+  __shared__ uint32_t s_off[kPartBuckets + 1];  // first entry of each bucket
+  __shared__ uint8_t s_bsz[kPartBuckets];   // bucket sizes before the call
+  __shared__ uint32_t s_rows[kBlock / 64][64];
   __shared__ uint32_t s_wsum[kBlock / 64];
   __shared__ uint32_t s_big;
   const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const uint32_t p = blockIdx.x;
   const uint32_t base_e = ps.pinfo[2 * p], m = ps.pinfo[2 * p + 1];
-  if (m > kPartLds) {
+  if (m > kFastLds) {
     if (tid == 0) ps.pflag[p] = 0;
+    return;
+  }
+  if (m == 0) {
+    if (tid == 0) ps.pflag[p] = 1;
     return;
   }
   const uint32_t B = t.B;
   const uint32_t R = t.row_bytes;
-  const uint64_t b = (uint64_t)p * kPartBuckets + tid;
-  const bool own = b < t.buckets;
-  const uint64_t base = b * (uint64_t)B;
-  // This lane's bucket state, fetched while the entries load.
-  DLine L;
-  int32_t bsz = 0;
-  gptr<uint8_t> rows0 = nullptr;
-  if (own) {
-    dl_load(L, G(t.digests) + base);
-    bsz = G(t.bsize)[b];
-    rows0 = row_ptr(t, b, 0);
-  }
-  gptr<const u64x2> ent = G(reinterpret_cast<const u64x2*>(ps.ent)) + base_e;
-  u64x2 ev[kPer];
-  uint32_t lb[kPer];
-#pragma unroll
-  for (uint32_t q = 0; q < kPer; q++) {
-    const uint32_t e = tid + q * kBlock;
-    if (e < m) {
-      ev[q] = ent[e];
-      lb[q] = (uint32_t)(bucket_of(t, ev[q].x) % kPartBuckets);
-    }
-  }
-  s_cnt[tid] = 0;
-  if (tid == 0) s_big = 0;
-  lds_barrier();
-#pragma unroll
-  for (uint32_t q = 0; q < kPer; q++)
-    if (tid + q * kBlock < m) atomicAdd(&s_cnt[lb[q]], 1u);
-  lds_barrier();
-  const uint32_t c = s_cnt[tid];
+  const uint64_t part_b0 = (uint64_t)p * kPartBuckets;
+  const bool has_in = a.in_scores != nullptr;
+  const bool old_for_hit = a.sc.strategy == kLfu || a.sc.strategy == kEpochLfu;
+  const bool old_for_new = a.sc.strategy == kLfu && !has_in;
+
+  /* A. Entries grouped by bucket (every load issued before the first use;
+        indices past m read entry m - 1 and are ignored). */
   {
+    const uint64_t b = part_b0 + tid;
+    const uint32_t bsz_own = b < t.buckets ? (uint32_t)G(t.bsize)[b] : 0u;
+    gptr<const u64x2> ent = G(reinterpret_cast<const u64x2*>(ps.ent)) + base_e;
+    u64x2 ev[kPer];
+    uint64_t inq[kPer];
+    uint32_t lb[kPer], pos[kPer];
+#pragma unroll
+    for (uint32_t q = 0; q < kPer; q++) {
+      const uint32_t e = tid + q * kBlock;
+      ev[q] = ent[e < m ? e : m - 1];
+    }
+#pragma unroll
+    for (uint32_t q = 0; q < kPer; q++) inq[q] = has_in ? G(a.in_scores)[ev[q].y] : 0;
+#pragma unroll
+    for (uint32_t q = 0; q < kPer; q++)
+      lb[q] = (uint32_t)(bucket_of(t, ev[q].x) % kPartBuckets);
+    s_cnt[tid] = 0;
+    s_bsz[tid] = (uint8_t)bsz_own;
+    if (tid == 0) s_big = 0;
+    lds_barrier();
+#pragma unroll
+    for (uint32_t q = 0; q < kPer; q++)
+      if (tid + q * kBlock < m) atomicAdd(&s_cnt[lb[q]], 1u);
+    lds_barrier();
+    const uint32_t c = s_cnt[tid];
     uint32_t x = c;
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
@@ -1763,176 +1876,356 @@ __global__ __launch_bounds__(kBlock) void k_apply_fast(TableView t, ApplyArgs a,
     lds_barrier();
     uint32_t pre = 0;
     for (uint32_t q = 0; q < wv; q++) pre += s_wsum[q];
-    s_off[tid] = pre + x - c;
-    s_fill[tid] = pre + x - c;
-  }
-  lds_barrier();
-  if (s_big) {
-    if (tid == 0) ps.pflag[p] = 0;  // a long bucket: k_apply_part orders it
-    return;
-  }
-  if (tid == 0) ps.pflag[p] = 1;
+    const uint32_t o = pre + x - c;
+    s_off[tid] = o;
+    s_cnt[tid] = o;  // fill pointer (this thread read its count above)
+    if (tid == 0) s_off[kPartBuckets] = m;
+    lds_barrier();
+    if (s_big) {
+      if (tid == 0) ps.pflag[p] = 0;  // a long bucket: k_apply_part orders it
+      return;
+    }
+    if (tid == 0) ps.pflag[p] = 1;
 #pragma unroll
-  for (uint32_t q = 0; q < kPer; q++) {
-    if (tid + q * kBlock < m) {
-      const uint32_t pos = atomicAdd(&s_fill[lb[q]], 1u);
-      s_key[pos] = ev[q].x;
-      s_idx[pos] = (uint32_t)ev[q].y;
-    }
-  }
-  lds_barrier();
-
-  // Lane pass over bucket b: its c keys sit at s_key/s_idx[o, o + c).
-  const uint32_t o = s_off[tid];
-  for (uint32_t x = 1; x < c; x++) {  // batch order (insertion sort)
-    const uint64_t kx = s_key[o + x];
-    const uint32_t ix = s_idx[o + x];
-    uint32_t y = x;
-    while (y > 0 && s_idx[o + y - 1] > ix) {
-      s_key[o + y] = s_key[o + y - 1];
-      s_idx[o + y] = s_idx[o + y - 1];
-      y--;
-    }
-    s_key[o + y] = kx;
-    s_idx[o + y] = ix;
-  }
-  const int32_t bsz0 = bsz;
-  const bool has_in = a.in_scores != nullptr;
-  gptr<uint64_t> trow = G(ps.trow);
-  constexpr bool may_insert = OP != OP_ASSIGN_SCORES;
-  uint32_t wr0 = 0, wr1 = 0, wr2 = 0, wr3 = 0;
-  uint32_t stop = c;  // first key left to the 16-lane kernel
-  for (uint32_t step = 0; step < c; step++) {
-    const uint64_t k = s_key[o + step];
-    const uint64_t i = s_idx[o + step];
-    const uint64_t in = has_in ? G(a.in_scores)[i] : 0;
-    const uint64_t h = murmur3(k);
-    const uint32_t start = (uint32_t)(global_idx(t, h) & (B - 1));
-    const uint32_t d = key_digest(h);
-    int dup = 0;
-    const int slot =
-        probe_upsert_reg(t, L, base, start, d, k, may_insert && bsz < (int32_t)B, &dup);
-    if (slot < 0 && may_insert) {
-      stop = step;
-      break;
-    }
-    uint64_t src = 0, dst = 0;
-    uint32_t res = 0;
-    if (slot >= 0) {
-      res = lane_apply<OP>(t, a, base, rows0, slot, dup, i, k, in, has_in, d, bsz, src, dst);
-      if (res & kLaneDigest) dl_set(L, (uint32_t)slot, d);
-    }
-    uint64_t task = 0;
-    uint8_t wrote = kNoSlot;
-    if (dst) {
-      const uint32_t sl = (uint32_t)slot;
-      const uint32_t bit = 1u << (sl & 31), wq = sl >> 5;
-      const uint32_t cur = wq == 0 ? wr0 : wq == 1 ? wr1 : wq == 2 ? wr2 : wr3;
-      // Latest earlier step of this bucket that wrote the row of `slot`.
-      uint32_t prev = kNone;
-      if (cur & bit)
-        for (uint32_t x = 0; x < step; x++)
-          if (s_slot[o + x] == (uint8_t)sl) prev = x;
-      if (res & kLaneRead) {
-        // A hit: read the row, or the input of the key that wrote it.
-        task = prev != kNone ? (kTaskFwd | s_idx[o + prev]) : (kTaskOut | (src & kTaskMask));
-      } else {
-        // The row is written: a later write of the same row supersedes.
-        if (prev != kNone) {
-          trow[s_idx[o + prev]] = 0;
-          s_slot[o + prev] = kNoSlot;
-        }
-        task = kTaskIn | (dst & kTaskMask);
-        wrote = (uint8_t)sl;
-        wr0 |= wq == 0 ? bit : 0u;
-        wr1 |= wq == 1 ? bit : 0u;
-        wr2 |= wq == 2 ? bit : 0u;
-        wr3 |= wq == 3 ? bit : 0u;
+    for (uint32_t q = 0; q < kPer; q++) {
+      if (tid + q * kBlock < m) {
+        pos[q] = atomicAdd(&s_cnt[lb[q]], 1u);
+        s_key[pos[q]] = ev[q].x;
+        s_idx[pos[q]] = (uint32_t)ev[q].y;
+        s_sc[pos[q]] = inq[q];
       }
     }
-    s_slot[o + step] = wrote;
-    if (task) trow[i] = task;
+    lds_barrier();
+    s_cnt[tid] = kNone;  // first rank the parallel pass does not apply (none yet)
+    // Rank of each entry in batch order inside its bucket.
+#pragma unroll
+    for (uint32_t q = 0; q < kPer; q++) {
+      if (tid + q * kBlock < m) {
+        const uint32_t lo = s_off[lb[q]], hi = s_off[lb[q] + 1];
+        const uint32_t iv = (uint32_t)ev[q].y;
+        uint32_t r = 0;
+        for (uint32_t y = lo; y < hi; y++) r += s_idx[y] < iv ? 1u : 0u;
+        s_rank[pos[q]] = (uint8_t)r;
+      }
+    }
   }
-  if (bsz != bsz0) G(t.bsize)[b] = bsz;
-  uint32_t added = (uint32_t)(bsz - bsz0);
-#pragma unroll
-  for (int d = 32; d > 0; d >>= 1) added += __shfl_xor(added, d, 64);
-  if (lane == 0 && added) atomicAdd(t.live, (unsigned long long)added);
 
-  // Buckets left to the eviction path: a record {bucket, keys, first key
-  // left, pool offset} and all the bucket's keys in batch order.
-  const bool defer = stop < c;
-  const uint64_t dm = __ballot(defer);
-  if (dm) {
-    uint32_t x = defer ? c : 0;  // inclusive prefix of pool entries
+  /* B. Outcome of every key on the table before the call, with the score,
+        metadata record and row task it has if the parallel pass applies it. */
+  {
+    u32x4 w0[kPer], w1[kPer];
+    uint64_t gi[kPer];
 #pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const uint32_t y = __shfl_up(x, d, 64);
-      if (lane >= (uint32_t)d) x += y;
+    for (uint32_t q = 0; q < kPer; q++) {
+      const uint32_t e = tid + q * kBlock;
+      w0[q] = w1[q] = u32x4{0, 0, 0, 0};
+      gi[q] = 0;
+      if (e < m) {
+        gi[q] = global_idx(t, murmur3(s_key[e]));
+        const uint32_t a4 = (uint32_t)(gi[q] & (B - 1)) & ~3u;
+        gptr<const u32x4> drow = (gptr<const u32x4>)(G(t.digests) + (gi[q] >> t.bshift) * B);
+        w0[q] = drow[a4 >> 4];
+        w1[q] = drow[((a4 >> 4) + 1) & (B / 16 - 1)];
+      }
     }
-    uint32_t rbase = 0, pbase = 0;
-    if (lane == 63) {
-      rbase = atomicAdd(&ps.dctr[0], (uint32_t)__popcll(dm));
-      pbase = atomicAdd(&ps.dctr[1], x);
+    WinProbe wp[kPer];
+    uint64_t k0[kPer], k1[kPer];  // keys at the first two digest matches
+#pragma unroll
+    for (uint32_t q = 0; q < kPer; q++) {
+      const uint32_t e = tid + q * kBlock;
+      k0[q] = k1[q] = 0;
+      wp[q] = WinProbe{0, kNone, kNone, false, true};
+      if (e < m) {
+        const uint64_t k = s_key[e];
+        const uint32_t d = key_digest(murmur3(k));
+        wp[q] = probe_window(w0[q], w1[q], (uint32_t)(gi[q] & (B - 1)), d, B);
+        const uint64_t base = (gi[q] >> t.bshift) * B;
+        if (wp[q].c0 != kNone) k0[q] = slot_key(t, base + wp[q].c0);
+        if (wp[q].c1 != kNone) k1[q] = slot_key(t, base + wp[q].c1);
+      }
     }
-    rbase = __shfl(rbase, 63, 64);
-    pbase = __shfl(pbase, 63, 64);
-    if (defer) {
-      const uint32_t r = rbase + __popcll(dm & ((1ull << lane) - 1));
-      const uint32_t po = pbase + x - c;
-      gptr<uint32_t> rec = G(ps.drec) + 4 * (uint64_t)r;
+#pragma unroll
+    for (uint32_t q = 0; q < kPer; q++) {
+      const uint32_t e = tid + q * kBlock;
+      if (e >= m) continue;
+      const uint64_t k = s_key[e];
+      const uint64_t in = s_sc[e];
+      const uint32_t lbk = (uint32_t)((gi[q] >> t.bshift) % kPartBuckets);
+      const bool empties = !may_insert || s_bsz[lbk] < B;
+      uint8_t fl = kResSlow, slot = kNoSlot;
+      uint64_t sc = 0;
+      // A verified digest match is the first one in probe order, so the key
+      // is present there whether or not the window reached an EMPTY slot.
+      const bool hit0 = wp[q].c0 != kNone && k0[q] == k;
+      const bool hit1 = !hit0 && wp[q].c1 != kNone && k1[q] == k;
+      if (hit0 || hit1 || (wp[q].found && !wp[q].over && empties)) {
+        const uint64_t des = score_desired(a.sc, has_in, in);
+        bool w;
+        if (hit0 || hit1) {
+          const bool first = hit0;
+          slot = (uint8_t)(first ? wp[q].c0 : wp[q].c1);
+          const uint64_t old =
+              old_for_hit ? slot_score(t, (gi[q] >> t.bshift) * B + slot) : 0;
+          const uint64_t ns = OP == OP_ASSIGN_SCORES ? score_wo_missed(a.sc, has_in, in, old, &w)
+                                                     : score_hit(a.sc, has_in, in, des, old, &w);
+          fl = kResDup | (w ? kMetaScore : 0);
+          sc = ns;
+          if (moves_rows) fl |= reads_rows ? kTkOut : kTkIn;
+        } else if (!may_insert) {
+          fl = 0;  // assign_scores: absent keys are a no-op
+        } else if (!old_for_new) {
+          slot = (uint8_t)wp[q].slot;
+          sc = score_new(a.sc, has_in, in, des, 0, &w);
+          fl = kResNew | kMetaKey | kTkIn;
+        }
+      }
+      s_slot[e] = slot;
+      s_fl[e] = fl;
+      if (fl != kResSlow) s_sc[e] = sc;
+    }
+  }
+  lds_barrier();
+
+  /* C. Per bucket, the first key whose parallel outcome may differ from the
+        sequential one. */
+#pragma unroll
+  for (uint32_t q = 0; q < kPer; q++) {
+    const uint32_t e = tid + q * kBlock;
+    if (e >= m) continue;
+    const uint64_t k = s_key[e];
+    const uint32_t lbk = (uint32_t)(bucket_of(t, k) % kPartBuckets);
+    const uint32_t lo = s_off[lbk], hi = s_off[lbk + 1];
+    const uint32_t r = s_rank[e];
+    const uint32_t res = s_fl[e] & kResMask;
+    bool bad = res == kResSlow;
+    uint32_t nnew = 0;
+    for (uint32_t x = lo; x < hi; x++) {
+      if (s_rank[x] >= r) continue;
+      if (s_key[x] == k) bad = true;
+      if ((s_fl[x] & kResMask) == kResNew) {
+        nnew++;
+        if (res == kResNew && s_slot[x] == s_slot[e]) bad = true;
+      }
+    }
+    if (res == kResNew && s_bsz[lbk] + nnew >= B) bad = true;
+    if (bad) atomicMin(&s_cnt[lbk], r);
+  }
+  lds_barrier();
+
+  /* S. The rest of a bucket whose parallel pass stopped, by its owner lane. */
+  uint32_t added = 0;
+  {
+    const uint32_t bk = tid;
+    const uint64_t b = part_b0 + bk;
+    const uint32_t lo = s_off[bk], hi = s_off[bk + 1], c = hi - lo;
+    uint32_t stop = s_cnt[bk] < c ? s_cnt[bk] : c;
+    uint32_t bsz = s_bsz[bk];
+    uint32_t f0 = 0, f1 = 0, f2 = 0, f3 = 0;  // slots filled by the call so far
+    for (uint32_t x = lo; x < hi; x++) {
+      if (s_rank[x] < stop && (s_fl[x] & kResMask) == kResNew) {
+        const uint32_t sl = s_slot[x], bit = 1u << (sl & 31), wq = sl >> 5;
+        f0 |= wq == 0 ? bit : 0u;
+        f1 |= wq == 1 ? bit : 0u;
+        f2 |= wq == 2 ? bit : 0u;
+        f3 |= wq == 3 ? bit : 0u;
+        bsz++;
+      }
+    }
+    const uint64_t base = b * (uint64_t)B;
+    for (uint32_t r = stop; r < c; r++) {
+      const uint32_t e = entry_of_rank(s_rank, lo, hi, r);
+      const uint64_t k = s_key[e];
+      const uint64_t i = s_idx[e];
+      const uint64_t in = has_in ? G(a.in_scores)[i] : 0;
+      const uint64_t h = murmur3(k);
+      const uint32_t start = (uint32_t)(global_idx(t, h) & (B - 1));
+      const uint32_t d = key_digest(h);
+      int dup = 0;
+      const int sl = probe_serial(t, base, f0, f1, f2, f3, s_key, s_slot, s_fl, s_rank, lo, hi, r,
+                                  start, d, k, !may_insert || bsz < B, &dup);
+      if (sl < 0 && may_insert) {
+        // The eviction path: the rest of the bucket goes to k_apply_deferred.
+        stop = r;
+        break;
+      }
+      stop = r + 1;
+      uint8_t fl = 0;
+      if (sl < 0 || (!may_insert && !dup)) {  // assign_scores: absent
+        s_slot[e] = kNoSlot;
+        s_fl[e] = 0;
+        continue;
+      }
+      const uint32_t slu = (uint32_t)sl;
+      const uint64_t des = score_desired(a.sc, has_in, in);
+      bool w;
+      // The latest earlier record of the call at this slot, and the latest
+      // earlier key whose input row is queued for it.
+      uint32_t xrec = kNone, xin = kNone, rrec = 0, rin = 0;
+      for (uint32_t x = lo; x < hi; x++) {
+        const uint32_t rx = s_rank[x];
+        if (rx >= r || s_slot[x] != slu) continue;
+        if ((s_fl[x] & kMetaMask) && (xrec == kNone || rx > rrec)) {
+          xrec = x;
+          rrec = rx;
+        }
+        if ((s_fl[x] & kTkMask) == kTkIn && (xin == kNone || rx > rin)) {
+          xin = x;
+          rin = rx;
+        }
+      }
+      if (dup) {
+        uint64_t old = 0;
+        if (old_for_hit) old = xrec != kNone ? s_sc[xrec] : slot_score(t, base + slu);
+        const uint64_t ns = OP == OP_ASSIGN_SCORES ? score_wo_missed(a.sc, has_in, in, old, &w)
+                                                   : score_hit(a.sc, has_in, in, des, old, &w);
+        fl = kResDup;
+        if (w) {
+          if (xrec != kNone) {
+            s_sc[xrec] = ns;  // one record per slot: the earlier one carries it
+          } else {
+            fl |= kMetaScore;
+            s_sc[e] = ns;
+          }
+        }
+        if (moves_rows) {
+          if (reads_rows) {
+            fl |= xin != kNone ? kTkFwd : kTkOut;
+          } else {
+            if (xin != kNone) s_fl[xin] &= (uint8_t)~kTkMask;  // a later write supersedes
+            fl |= kTkIn;
+          }
+        }
+      } else {
+        const uint64_t old = old_for_new ? slot_score(t, base + slu) : 0;
+        const uint64_t ns = score_new(a.sc, has_in, in, des, old, &w);
+        s_sc[e] = w ? ns : old;
+        fl = kResNew | kMetaKey | kTkIn;
+        const uint32_t bit = 1u << (slu & 31), wq = slu >> 5;
+        f0 |= wq == 0 ? bit : 0u;
+        f1 |= wq == 1 ? bit : 0u;
+        f2 |= wq == 2 ? bit : 0u;
+        f3 |= wq == 3 ? bit : 0u;
+        bsz++;
+      }
+      s_slot[e] = (uint8_t)slu;
+      s_fl[e] = fl;
+    }
+    if (lo < hi) s_cnt[bk] = stop;  // keys of rank < stop are applied here
+    if (stop < c) {
+      // Hand over: a record {bucket, keys, first key left, pool offset} and
+      // the bucket's keys in batch order.
+      const uint32_t rb = atomicAdd(&ps.dctr[0], 1u);
+      const uint32_t po = atomicAdd(&ps.dctr[1], c);
+      gptr<uint32_t> rec = G(ps.drec) + 4 * (uint64_t)rb;
       rec[0] = (uint32_t)b;
       rec[1] = c;
       rec[2] = stop;
       rec[3] = po;
       gptr<u64x2> pool = G(reinterpret_cast<u64x2*>(ps.dpool)) + po;
-      for (uint32_t q = 0; q < c; q++) {
+      for (uint32_t x = lo; x < hi; x++) {
         u64x2 v;
-        v.x = s_key[o + q];
-        v.y = s_idx[o + q];
-        pool[q] = v;
+        v.x = s_key[x];
+        v.y = s_idx[x];
+        pool[s_rank[x]] = v;
       }
+    }
+    if (lo < hi && bsz != s_bsz[bk]) {
+      G(t.bsize)[b] = (int32_t)bsz;
+      added = bsz - s_bsz[bk];
+    }
+  }
+  lds_barrier();
+
+  /* W. Metadata of the applied keys: at most one record per slot. */
+#pragma unroll
+  for (uint32_t q = 0; q < kPer; q++) {
+    const uint32_t e = tid + q * kBlock;
+    if (e >= m) continue;
+    const uint32_t f = s_fl[e] & kMetaMask;
+    if (!f) continue;
+    const uint64_t k = s_key[e];
+    const uint64_t h = murmur3(k);
+    const uint64_t gb = global_idx(t, h) >> t.bshift;
+    if (s_rank[e] >= s_cnt[gb % kPartBuckets]) continue;  // left to k_apply_deferred
+    const uint64_t s = gb * B + s_slot[e];
+    if (f == kMetaKey) {
+      slot_store(t, s, k, s_sc[e]);
+      G(t.digests)[s] = (uint8_t)key_digest(h);
+    } else {
+      slot_score(t, s) = s_sc[e];
+    }
+  }
+#pragma unroll
+  for (int d = 32; d > 0; d >>= 1) added += __shfl_xor(added, d, 64);
+  if (lane == 0) s_wsum[wv] = added;
+  lds_barrier();
+  if (tid == 0) {
+    uint32_t tot = 0;
+    for (uint32_t q = 0; q < kBlock / 64; q++) tot += s_wsum[q];
+    if (tot) atomicAdd(t.live, (unsigned long long)tot);
+  }
+
+  // Row copies of the block's tasks.  Tasks of different keys name different
+  // rows (a superseded write was dropped above), except that a forwarded
+  // read takes an input row that is only read, so they run in any order.
+  if (moves_rows) {
+    const uint64_t R64 = R;
+    for (uint32_t e0 = 0; e0 < m; e0 += kBlock) {
+      const uint32_t e = e0 + tid;
+      uint64_t src = 0, dst = 0;
+      uint32_t tk = e < m ? (s_fl[e] & kTkMask) : 0u;
+      uint64_t gb = 0;
+      if (tk) {
+        gb = bucket_of(t, s_key[e]);
+        if (s_rank[e] >= s_cnt[gb % kPartBuckets]) tk = 0;
+      }
+      if (tk) {
+        const uint64_t i = s_idx[e];
+        const uint32_t sl = s_slot[e];
+        const uint64_t trow = (uint64_t)(uintptr_t)row_ptr(t, gb, sl);
+        if (tk == kTkIn) {
+          src = (uint64_t)(uintptr_t)(a.in_values + i * R64);
+          dst = trow;
+        } else if (tk == kTkOut) {
+          src = trow;
+          dst = (uint64_t)(uintptr_t)(a.io_values + i * R64);
+        } else {
+          // The latest earlier key of the bucket whose input row was
+          // queued for this slot.
+          const uint32_t lbk = (uint32_t)(gb % kPartBuckets);
+          const uint32_t lo = s_off[lbk], hi = s_off[lbk + 1], r = s_rank[e];
+          uint32_t xs = e, rs = 0;
+          for (uint32_t x = lo; x < hi; x++) {
+            const uint32_t rx = s_rank[x];
+            if (rx < r && s_slot[x] == sl && (s_fl[x] & kTkMask) == kTkIn && (xs == e || rx > rs)) {
+              xs = x;
+              rs = rx;
+            }
+          }
+          src = (uint64_t)(uintptr_t)(a.io_values + (uint64_t)s_idx[xs] * R64);
+          dst = (uint64_t)(uintptr_t)(a.io_values + i * R64);
+        }
+      }
+      wave_copy_pairs_q<U, 4>(src, dst, R, s_rows[wv]);
     }
   }
 }
 
-// One 16-lane group per bucket handed over by k_apply_fast: first the row
-// tasks recorded for the keys the lane already applied, then the remaining
-// keys through the eviction path, in batch order.
+// One 16-lane group per bucket handed over by k_apply_fast, which applied
+// (and copied the rows of) the bucket's keys before `st`: the remaining keys
+// go through the eviction path, in batch order.
 template <int OP, int U>
 __global__ __launch_bounds__(kBlock) void k_apply_deferred(TableView t, ApplyArgs a,
                                                            PartScratch ps) {
   const uint32_t nrec = *(volatile uint32_t*)ps.dctr;
   const uint32_t gl = threadIdx.x & 15;
   const uint64_t ngroups = (uint64_t)gridDim.x * (kBlock / 16);
-  const uint32_t R = t.row_bytes;
-  gptr<uint64_t> trow = G(ps.trow);
   gptr<const u64x2> pool = G(reinterpret_cast<const u64x2*>(ps.dpool));
   for (uint64_t r = ((uint64_t)blockIdx.x * kBlock + threadIdx.x) >> 4; r < nrec;
        r += ngroups) {
     gptr<const uint32_t> rec = G(ps.drec) + 4 * r;
     const uint64_t b = rec[0];
     const uint32_t c = rec[1], st = rec[2], po = rec[3];
-    for (uint32_t x = 0; x < st; x++) {
-      const uint64_t i = pool[po + x].y;
-      const uint64_t tv = trow[i];
-      if (tv == 0) continue;
-      const uint64_t kind = tv & ~kTaskMask, val = tv & kTaskMask;
-      gptr<const uint8_t> src;
-      gptr<uint8_t> dst;
-      if (kind == kTaskIn) {
-        src = G(a.in_values) + i * (uint64_t)R;
-        dst = G<uint8_t>((uintptr_t)val);
-      } else if (kind == kTaskOut) {
-        src = G<const uint8_t>((uintptr_t)val);
-        dst = G(a.io_values) + i * (uint64_t)R;
-      } else {
-        src = G(a.io_values) + val * (uint64_t)R;
-        dst = G(a.io_values) + i * (uint64_t)R;
-      }
-      copy_units<U>(dst, src, R, gl, 16);
-      if (gl == 0) trow[i] = 0;
-    }
     Bucket16 S;
     bucket_load(t, S, b, gl);
     for (uint32_t step = st; step < c; step++) {
@@ -1941,16 +2234,6 @@ __global__ __launch_bounds__(kBlock) void k_apply_deferred(TableView t, ApplyArg
     }
     bucket_finish(t, S);
   }
-}
-
-// Executes the row tasks k_apply_part left, one batch index per lane.
-template <int U>
-__global__ __launch_bounds__(kBlock) void k_rowcopy(ApplyArgs a, uint64_t* __restrict__ trow,
-                                                    uint32_t row_bytes) {
-  __shared__ uint32_t s_rows[kBlock / 64][64];
-  const uint32_t wv = threadIdx.x >> 6;
-  const uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
-  wave_run_tasks<U>(a, G(trow), i, i < a.n, row_bytes, s_rows[wv]);
 }
 
 /* ------------------------------------------------------------------------ */
@@ -2282,15 +2565,13 @@ static void apply_part_op(const TableView& t, const ApplyArgs& a, const PartScra
   hipLaunchKernelGGL(k_pscatter, dim3(ps.chunks), dim3(kBlock), lds, s, t, a.keys, a.n, ps);
   const dim3 g(ps.np), b(kBlock);
   constexpr bool fast = OP != OP_ACCUM_OR_ASSIGN;
-  const bool rows = OP != OP_ACCUM_OR_ASSIGN && OP != OP_ASSIGN_SCORES;
-  const dim3 gr(grid_for(a.n, kBlock, 1ull << 31));
   const dim3 gd(grid_for(a.n * 16, kBlock, 4096));
-  if constexpr (fast) hipLaunchKernelGGL((k_apply_fast<fast ? OP : 0>), g, b, 0, s, t, a, ps);
 #define HKV_PART_U(UU)                                                                       \
-  if constexpr (fast)                                                                        \
+  if constexpr (fast) {                                                                      \
+    hipLaunchKernelGGL((k_apply_fast<fast ? OP : 0, UU>), g, b, 0, s, t, a, ps);             \
     hipLaunchKernelGGL((k_apply_deferred<fast ? OP : 0, UU>), gd, b, 0, s, t, a, ps);        \
-  hipLaunchKernelGGL((k_apply_part<OP, UU>), g, b, 0, s, t, a, ps, fast ? 0 : 1);            \
-  if (rows) hipLaunchKernelGGL((k_rowcopy<UU>), gr, b, 0, s, a, ps.trow, t.row_bytes)
+  }                                                                                          \
+  hipLaunchKernelGGL((k_apply_part<OP, UU>), g, b, 0, s, t, a, ps, fast ? 0 : 1)
   switch (a.unit) {
     case 16: HKV_PART_U(16); break;
     case 8: HKV_PART_U(8); break;
