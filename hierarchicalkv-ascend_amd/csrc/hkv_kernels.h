@@ -56,10 +56,10 @@ struct PartScratch {
   uint32_t* pinfo;      // [partitions][2]: first entry, entry count
   uint32_t* spill_top;  // entries placed past the fixed regions
   uint64_t* trow;       // [n] row task per batch index, zero between calls
-  uint32_t* pflag;      // [partitions] 1 = applied by the single-run kernel
+  uint32_t* plist;      // [partitions] partitions the single-run kernel left
   uint32_t* drec;       // [n][4] buckets handed to the 16-lane kernel
   uint64_t* dpool;      // [n][2] their keys, {key, batch index}
-  uint32_t* dctr;       // [2] records, pool entries (zeroed by the count kernel)
+  uint32_t* dctr;       // [3] records, pool entries, listed partitions (zeroed by the count kernel)
   uint32_t np;          // partitions
   uint32_t chunks;      // batch chunks
   uint32_t cap;         // fixed region size per partition (entries)

@@ -133,7 +133,8 @@ __device__ __forceinline__ bool use_key_first(const TableView& t) {
 // dst_base + (lane_base + lane) * row_bytes.  The wave is split into groups of
 // lpr lanes, one row per group; each pass moves four rows per group with all
 // loads issued before the stores.  Rows past `rows` load row lds_rows[0]
-// (valid) and store nothing.
+// (valid) and store nothing.  Rows are streamed with non-temporal loads and
+// stores, which keeps the probed metadata lines in the L2 cache.
 template <int U>
 __device__ __forceinline__ void wave_copy_rows(uint32_t rows, const uint32_t* lds_rows,
                                                gptr<const uint8_t> src, uint8_t* dst_base,
@@ -161,11 +162,12 @@ __device__ __forceinline__ void wave_copy_rows(uint32_t rows, const uint32_t* ld
     gptr<T> d2 = G(reinterpret_cast<T*>(dst_base + (lane_base + l2) * row_bytes));
     gptr<T> d3 = G(reinterpret_cast<T*>(dst_base + (lane_base + l3) * row_bytes));
     for (uint32_t u = sub; u < units; u += lpr) {
-      const T v0 = s0[u], v1 = s1[u], v2 = s2[u], v3 = s3[u];
-      if (ok0) d0[u] = v0;
-      if (ok1) d1[u] = v1;
-      if (ok2) d2[u] = v2;
-      if (ok3) d3[u] = v3;
+      const T v0 = __builtin_nontemporal_load(&s0[u]), v1 = __builtin_nontemporal_load(&s1[u]),
+              v2 = __builtin_nontemporal_load(&s2[u]), v3 = __builtin_nontemporal_load(&s3[u]);
+      if (ok0) __builtin_nontemporal_store(v0, &d0[u]);
+      if (ok1) __builtin_nontemporal_store(v1, &d1[u]);
+      if (ok2) __builtin_nontemporal_store(v2, &d2[u]);
+      if (ok3) __builtin_nontemporal_store(v3, &d3[u]);
     }
   }
 }
@@ -1098,22 +1100,26 @@ __device__ __forceinline__ uint64_t bucket_of(const TableView& t, uint64_t k) {
 __global__ __launch_bounds__(kBlock) void k_pcount(TableView t, const uint64_t* __restrict__ keys,
                                                    uint64_t n, PartScratch ps) {
   extern __shared__ uint32_t s_h[];
+  constexpr uint32_t kPer = kPartChunk / kBlock;
   const uint32_t NP = ps.np;
+  const uint64_t i0 = (uint64_t)blockIdx.x * kPartChunk;
+  uint64_t kq[kPer];
+#pragma unroll
+  for (uint32_t q = 0; q < kPer; q++) {
+    const uint64_t i = i0 + threadIdx.x + q * kBlock;
+    kq[q] = i < n ? keys[i] : kEmptyKey;  // reserved: not counted
+  }
   for (uint32_t q = threadIdx.x; q < NP; q += kBlock) s_h[q] = 0;
   if (blockIdx.x == 0 && threadIdx.x == 0) {
     *ps.spill_top = 0;
     ps.dctr[0] = 0;
     ps.dctr[1] = 0;
+    ps.dctr[2] = 0;
   }
   __syncthreads();
-  const uint64_t i0 = (uint64_t)blockIdx.x * kPartChunk;
-  for (uint32_t j = threadIdx.x; j < kPartChunk; j += kBlock) {
-    const uint64_t i = i0 + j;
-    if (i < n) {
-      const uint64_t k = keys[i];
-      if (!is_reserved(k)) atomicAdd(&s_h[bucket_of(t, k) / kPartBuckets], 1u);
-    }
-  }
+#pragma unroll
+  for (uint32_t q = 0; q < kPer; q++)
+    if (!is_reserved(kq[q])) atomicAdd(&s_h[bucket_of(t, kq[q]) / kPartBuckets], 1u);
   __syncthreads();
   uint32_t* H = ps.hist + (uint64_t)blockIdx.x * NP;
   for (uint32_t q = threadIdx.x; q < NP; q += kBlock) H[q] = s_h[q];
@@ -1125,6 +1131,7 @@ __global__ __launch_bounds__(kBlock) void k_pcount(TableView t, const uint64_t* 
 constexpr uint32_t kScanGroups = 64;
 
 __global__ __launch_bounds__(1024) void k_pscan(PartScratch ps) {
+  constexpr uint32_t kReg = 16;  // column values a thread keeps in registers
   __shared__ uint32_t s_part[kScanGroups][16];
   __shared__ uint32_t s_base[16];
   const uint32_t c = threadIdx.x & 15, sg = threadIdx.x >> 4;
@@ -1134,9 +1141,17 @@ __global__ __launch_bounds__(1024) void k_pscan(PartScratch ps) {
   const uint32_t g0 = sg * per < NG ? sg * per : NG;
   const uint32_t g1 = g0 + per < NG ? g0 + per : NG;
   const bool live = p < NP;
+  const bool in_reg = per <= kReg;
   gptr<uint32_t> col = G(ps.hist) + p;
+  uint32_t v[kReg];
   uint32_t sum = 0;
-  if (live) {
+  if (live && in_reg) {
+#pragma unroll
+    for (uint32_t j = 0; j < kReg; j++) {
+      v[j] = g0 + j < g1 ? col[(uint64_t)(g0 + j) * NP] : 0u;
+      sum += v[j];
+    }
+  } else if (live) {
 #pragma unroll 8
     for (uint32_t g = g0; g < g1; g++) sum += col[(uint64_t)g * NP];
   }
@@ -1155,11 +1170,19 @@ __global__ __launch_bounds__(1024) void k_pscan(PartScratch ps) {
   if (live) {
     uint32_t off = s_base[c];
     for (uint32_t q = 0; q < sg; q++) off += s_part[q][c];
+    if (in_reg) {
+#pragma unroll
+      for (uint32_t j = 0; j < kReg; j++) {
+        if (g0 + j < g1) col[(uint64_t)(g0 + j) * NP] = off;
+        off += v[j];
+      }
+    } else {
 #pragma unroll 8
-    for (uint32_t g = g0; g < g1; g++) {
-      const uint32_t v = col[(uint64_t)g * NP];
-      col[(uint64_t)g * NP] = off;
-      off += v;
+      for (uint32_t g = g0; g < g1; g++) {
+        const uint32_t x = col[(uint64_t)g * NP];
+        col[(uint64_t)g * NP] = off;
+        off += x;
+      }
     }
   }
 }
@@ -1168,24 +1191,28 @@ __global__ __launch_bounds__(kBlock) void k_pscatter(TableView t,
                                                      const uint64_t* __restrict__ keys,
                                                      uint64_t n, PartScratch ps) {
   extern __shared__ uint32_t s_o[];
+  constexpr uint32_t kPer = kPartChunk / kBlock;
   const uint32_t NP = ps.np;
+  const uint64_t i0 = (uint64_t)blockIdx.x * kPartChunk;
+  // The chunk's keys and its row of segment offsets load together.
+  uint64_t kq[kPer];
+#pragma unroll
+  for (uint32_t q = 0; q < kPer; q++) {
+    const uint64_t i = i0 + threadIdx.x + q * kBlock;
+    kq[q] = i < n ? keys[i] : kEmptyKey;  // reserved: skipped
+  }
   const uint32_t* H = ps.hist + (uint64_t)blockIdx.x * NP;
   for (uint32_t q = threadIdx.x; q < NP; q += kBlock) s_o[q] = H[q];
   __syncthreads();
-  const uint64_t i0 = (uint64_t)blockIdx.x * kPartChunk;
   gptr<u64x2> ent = G(reinterpret_cast<u64x2*>(ps.ent));
-  for (uint32_t j = threadIdx.x; j < kPartChunk; j += kBlock) {
-    const uint64_t i = i0 + j;
-    if (i < n) {
-      const uint64_t k = keys[i];
-      if (!is_reserved(k)) {
-        const uint32_t pos = atomicAdd(&s_o[bucket_of(t, k) / kPartBuckets], 1u);
-        u64x2 v;
-        v.x = k;
-        v.y = i;
-        ent[pos] = v;
-      }
-    }
+#pragma unroll
+  for (uint32_t q = 0; q < kPer; q++) {
+    if (is_reserved(kq[q])) continue;
+    const uint32_t pos = atomicAdd(&s_o[bucket_of(t, kq[q]) / kPartBuckets], 1u);
+    u64x2 v;
+    v.x = kq[q];
+    v.y = i0 + threadIdx.x + q * kBlock;
+    ent[pos] = v;
   }
 }
 
@@ -1245,6 +1272,9 @@ __device__ __forceinline__ void wave_copy_pairs(uint64_t src, uint64_t dst, uint
 
 // wave_copy_pairs with Q rows per lane group in flight: all loads of a round
 // are issued before its first store, and rows past the end are not touched.
+// The rows are streamed with non-temporal loads and stores, so that they do
+// not evict the bucket metadata other keys of the call are probing from the
+// L2 cache.
 template <int U, int Q>
 __device__ __forceinline__ void wave_copy_pairs_q(uint64_t src, uint64_t dst, uint32_t row_bytes,
                                                   uint32_t* s_rows) {
@@ -1275,10 +1305,10 @@ __device__ __forceinline__ void wave_copy_pairs_q(uint64_t src, uint64_t dst, ui
       T v[Q];
 #pragma unroll
       for (int q = 0; q < Q; q++)
-        if (ok[q]) v[q] = s[q][u];
+        if (ok[q]) v[q] = __builtin_nontemporal_load(&s[q][u]);
 #pragma unroll
       for (int q = 0; q < Q; q++)
-        if (ok[q]) d[q][u] = v[q];
+        if (ok[q]) __builtin_nontemporal_store(v[q], &d[q][u]);
     }
   }
   __builtin_amdgcn_wave_barrier();
@@ -1334,308 +1364,312 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
   __shared__ uint64_t s_dst[kBlock / 64][kQ];
   __shared__ uint32_t s_ndefer, s_c1, s_g;
   const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const uint32_t p = blockIdx.x;
   const uint32_t NP = ps.np, NG = ps.chunks;
-  if (!all && ps.pflag[p]) return;  // applied by k_apply_fast
-  const uint32_t base_e = ps.pinfo[2 * p], m = ps.pinfo[2 * p + 1];
   const uint32_t B = t.B;
-  const uint64_t part_b0 = (uint64_t)p * kPartBuckets;
   const uint32_t R = t.row_bytes;
   const bool has_in = a.in_scores != nullptr;
   gptr<const u64x2> ent = G(reinterpret_cast<const u64x2*>(ps.ent));
   gptr<uint64_t> trow = G(ps.trow);
   uint32_t added = 0;
-  if (tid == 0) s_g = 0;
-  uint32_t c0 = base_e;
-  const uint32_t end_e = base_e + m;
-  while (c0 < end_e) {
-    // This run of entries: the whole partition when it fits, else whole
-    // segments in chunk order.
-    if (tid == 0) {
-      uint32_t c1 = end_e;
-      if (m > kPartLds) {
-        uint32_t g = s_g;
-        c1 = c0;
-        while (g < NG) {
-          const uint32_t e = g + 1 < NG ? ps.hist[(uint64_t)(g + 1) * NP + p] : end_e;
-          if (e - c0 > kPartLds) break;
-          c1 = e;
-          g++;
+  // Every partition (accum_or_assign), else the ones k_apply_fast left.
+  const uint32_t nlist = all ? NP : *(volatile uint32_t*)&ps.dctr[2];
+  for (uint32_t li = blockIdx.x; li < nlist; li += gridDim.x) {
+    const uint32_t p = all ? li : ps.plist[li];
+    const uint32_t base_e = ps.pinfo[2 * p], m = ps.pinfo[2 * p + 1];
+    const uint64_t part_b0 = (uint64_t)p * kPartBuckets;
+    if (tid == 0) s_g = 0;
+    uint32_t c0 = base_e;
+    const uint32_t end_e = base_e + m;
+    while (c0 < end_e) {
+      // This run of entries: the whole partition when it fits, else whole
+      // segments in chunk order.
+      if (tid == 0) {
+        uint32_t c1 = end_e;
+        if (m > kPartLds) {
+          uint32_t g = s_g;
+          c1 = c0;
+          while (g < NG) {
+            const uint32_t e = g + 1 < NG ? ps.hist[(uint64_t)(g + 1) * NP + p] : end_e;
+            if (e - c0 > kPartLds) break;
+            c1 = e;
+            g++;
+          }
+          s_g = g;
         }
-        s_g = g;
+        s_c1 = c1;
+        s_ndefer = 0;
       }
-      s_c1 = c1;
-      s_ndefer = 0;
-    }
-    s_cnt[tid] = 0;
-    if (tid < 64) s_cls[tid] = 0;
-    __syncthreads();
-    const uint32_t c1 = s_c1;
-    const uint32_t mc = c1 - c0;
-    // Group the run's entries by bucket.
-    for (uint32_t e = tid; e < mc; e += kBlock)
-      atomicAdd(&s_cnt[bucket_of(t, ent[c0 + e].x) % kPartBuckets], 1u);
-    __syncthreads();
-    {
-      const uint32_t v = s_cnt[tid];
-      uint32_t x = v;
-#pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const uint32_t y = __shfl_up(x, d, 64);
-        if (lane >= (uint32_t)d) x += y;
-      }
-      if (lane == 63) s_wsum[wv] = x;
+      s_cnt[tid] = 0;
+      if (tid < 64) s_cls[tid] = 0;
       __syncthreads();
-      uint32_t pre = 0;
-      for (uint32_t q = 0; q < wv; q++) pre += s_wsum[q];
-      s_off[tid] = pre + x - v;
-      s_fill[tid] = pre + x - v;
-    }
-    __syncthreads();
-    for (uint32_t e = tid; e < mc; e += kBlock) {
-      const u64x2 v = ent[c0 + e];
-      const uint32_t pos = atomicAdd(&s_fill[bucket_of(t, v.x) % kPartBuckets], 1u);
-      s_key[pos] = v.x;
-      s_idx[pos] = (uint32_t)v.y;
-    }
-    if (kDeferRows) {
-      // Digest rows of the partition's buckets (one contiguous region).
-      gptr<const u32x4> dsrc = (gptr<const u32x4>)(G(t.digests) + part_b0 * B);
-      const uint32_t nbk =
-          t.buckets - part_b0 < kPartBuckets ? (uint32_t)(t.buckets - part_b0) : kPartBuckets;
-      for (uint32_t q = tid; q < nbk * 8; q += kBlock) {
-        const u32x4 v = dsrc[q];
-        uint32_t* row = s_dg + (q >> 3) * kDgStride + (q & 7) * 4;
-        row[0] = v.x;
-        row[1] = v.y;
-        row[2] = v.z;
-        row[3] = v.w;
-      }
-    }
-    __syncthreads();
-    if (kDeferRows) {
-      // Lanes take buckets in decreasing order of key count, so that a wave
-      // holds buckets of similar work (counts above 63 tie).
-      const uint32_t cc = s_cnt[tid] < 63 ? s_cnt[tid] : 63;
-      const uint32_t r = atomicAdd(&s_cls[63 - cc], 1u);
+      const uint32_t c1 = s_c1;
+      const uint32_t mc = c1 - c0;
+      // Group the run's entries by bucket.
+      for (uint32_t e = tid; e < mc; e += kBlock)
+        atomicAdd(&s_cnt[bucket_of(t, ent[c0 + e].x) % kPartBuckets], 1u);
       __syncthreads();
-      // Exclusive prefix of the 64 count classes, by one wave.
-      if (wv == 0) {
-        const uint32_t v = s_cls[lane];
+      {
+        const uint32_t v = s_cnt[tid];
         uint32_t x = v;
 #pragma unroll
         for (int d = 1; d < 64; d <<= 1) {
           const uint32_t y = __shfl_up(x, d, 64);
           if (lane >= (uint32_t)d) x += y;
         }
-        s_defer[lane] = x - v;  // class offsets (s_defer is free here)
+        if (lane == 63) s_wsum[wv] = x;
+        __syncthreads();
+        uint32_t pre = 0;
+        for (uint32_t q = 0; q < wv; q++) pre += s_wsum[q];
+        s_off[tid] = pre + x - v;
+        s_fill[tid] = pre + x - v;
       }
       __syncthreads();
-      s_perm[s_defer[63 - cc] + r] = tid;
-      __syncthreads();
-    }
-
-    // Lane pass: the lane owns bucket bk of the partition.
-    const uint32_t bk = kDeferRows ? s_perm[tid] : tid;
-    const uint64_t b = part_b0 + bk;
-    const bool own = b < t.buckets;
-    const uint32_t c = own ? s_cnt[bk] : 0;
-    const uint32_t o = s_off[bk];
-    const bool lane_ok = c > 0 && c <= kLaneMax;
-    if (lane_ok) {
-      // Batch order within the bucket (insertion sort of a short run).
-      for (uint32_t x = 1; x < c; x++) {
-        const uint64_t kx = s_key[o + x];
-        const uint32_t ix = s_idx[o + x];
-        uint32_t y = x;
-        while (y > 0 && s_idx[o + y - 1] > ix) {
-          s_key[o + y] = s_key[o + y - 1];
-          s_idx[o + y] = s_idx[o + y - 1];
-          y--;
+      for (uint32_t e = tid; e < mc; e += kBlock) {
+        const u64x2 v = ent[c0 + e];
+        const uint32_t pos = atomicAdd(&s_fill[bucket_of(t, v.x) % kPartBuckets], 1u);
+        s_key[pos] = v.x;
+        s_idx[pos] = (uint32_t)v.y;
+      }
+      if (kDeferRows) {
+        // Digest rows of the partition's buckets (one contiguous region).
+        gptr<const u32x4> dsrc = (gptr<const u32x4>)(G(t.digests) + part_b0 * B);
+        const uint32_t nbk =
+            t.buckets - part_b0 < kPartBuckets ? (uint32_t)(t.buckets - part_b0) : kPartBuckets;
+        for (uint32_t q = tid; q < nbk * 8; q += kBlock) {
+          const u32x4 v = dsrc[q];
+          uint32_t* row = s_dg + (q >> 3) * kDgStride + (q & 7) * 4;
+          row[0] = v.x;
+          row[1] = v.y;
+          row[2] = v.z;
+          row[3] = v.w;
         }
-        s_key[o + y] = kx;
-        s_idx[o + y] = ix;
       }
-    } else if (c > kLaneMax) {
-      s_defer[atomicAdd(&s_ndefer, 1u)] = bk << 16;
-    }
-    const uint64_t base = b * (uint64_t)B;
-    int32_t bsz = lane_ok ? G(t.bsize)[b] : 0;
-    const int32_t bsz0 = bsz;
-    uint32_t wr0 = 0, wr1 = 0, wr2 = 0, wr3 = 0;
-    if constexpr (kDeferRows) {
+      __syncthreads();
+      if (kDeferRows) {
+        // Lanes take buckets in decreasing order of key count, so that a wave
+        // holds buckets of similar work (counts above 63 tie).
+        const uint32_t cc = s_cnt[tid] < 63 ? s_cnt[tid] : 63;
+        const uint32_t r = atomicAdd(&s_cls[63 - cc], 1u);
+        __syncthreads();
+        // Exclusive prefix of the 64 count classes, by one wave.
+        if (wv == 0) {
+          const uint32_t v = s_cls[lane];
+          uint32_t x = v;
+#pragma unroll
+          for (int d = 1; d < 64; d <<= 1) {
+            const uint32_t y = __shfl_up(x, d, 64);
+            if (lane >= (uint32_t)d) x += y;
+          }
+          s_defer[lane] = x - v;  // class offsets (s_defer is free here)
+        }
+        __syncthreads();
+        s_perm[s_defer[63 - cc] + r] = tid;
+        __syncthreads();
+      }
+
+      // Lane pass: the lane owns bucket bk of the partition.
+      const uint32_t bk = kDeferRows ? s_perm[tid] : tid;
+      const uint64_t b = part_b0 + bk;
+      const bool own = b < t.buckets;
+      const uint32_t c = own ? s_cnt[bk] : 0;
+      const uint32_t o = s_off[bk];
+      const bool lane_ok = c > 0 && c <= kLaneMax;
       if (lane_ok) {
-        uint32_t* dg = s_dg + bk * kDgStride;
-        const gptr<uint8_t> rows0 = row_ptr(t, b, 0);
-        constexpr bool may_insert = OP != OP_ASSIGN_SCORES;
-        for (uint32_t step = 0; step < c; step++) {
-          const uint64_t k = s_key[o + step];
-          const uint64_t i = s_idx[o + step];
-          const uint64_t in = has_in ? G(a.in_scores)[i] : 0;
-          const uint64_t h = murmur3(k);
-          const uint32_t start = (uint32_t)(global_idx(t, h) & (B - 1));
-          const uint32_t d = key_digest(h);
-          int dup = 0;
-          const int slot =
-              probe_upsert_lds(t, dg, base, start, d, k, may_insert && bsz < (int32_t)B, &dup);
-          if (slot < 0 && may_insert) {
-            // Eviction path: the 16-lane pass resumes here, after running the
-            // row tasks recorded so far for this bucket.
-            s_defer[atomicAdd(&s_ndefer, 1u)] = (bk << 16) | step;
-            break;
+        // Batch order within the bucket (insertion sort of a short run).
+        for (uint32_t x = 1; x < c; x++) {
+          const uint64_t kx = s_key[o + x];
+          const uint32_t ix = s_idx[o + x];
+          uint32_t y = x;
+          while (y > 0 && s_idx[o + y - 1] > ix) {
+            s_key[o + y] = s_key[o + y - 1];
+            s_idx[o + y] = s_idx[o + y - 1];
+            y--;
           }
-          uint64_t src = 0, dst = 0;
-          uint32_t res = 0;
-          if (slot >= 0) {
-            res = lane_apply<OP>(t, a, base, rows0, slot, dup, i, k, in, has_in, d, bsz, src,
-                                 dst);
-            if (res & kLaneDigest) reinterpret_cast<uint8_t*>(dg)[slot] = (uint8_t)d;
-          }
-          uint64_t task = 0;
-          uint8_t wrote = kNoSlot;
-          if (dst) {
-            const uint32_t sl = (uint32_t)slot;
-            const uint32_t bit = 1u << (sl & 31), wq = sl >> 5;
-            const uint32_t cur = wq == 0 ? wr0 : wq == 1 ? wr1 : wq == 2 ? wr2 : wr3;
-            // Latest earlier step of this bucket that wrote the row of `slot`.
-            uint32_t prev = kNone;
-            if (cur & bit)
-              for (uint32_t x = 0; x < step; x++)
-                if (s_slot[o + x] == (uint8_t)sl) prev = x;
-            if (res & kLaneRead) {
-              // A hit: read the row, or the input of the key that wrote it.
-              task = prev != kNone ? (kTaskFwd | s_idx[o + prev])
-                                   : (kTaskOut | (src & kTaskMask));
-            } else {
-              // The row is written: a later write of the same row supersedes.
-              if (prev != kNone) {
-                trow[s_idx[o + prev]] = 0;
-                s_slot[o + prev] = kNoSlot;
-              }
-              task = kTaskIn | (dst & kTaskMask);
-              wrote = (uint8_t)sl;
-              wr0 |= wq == 0 ? bit : 0u;
-              wr1 |= wq == 1 ? bit : 0u;
-              wr2 |= wq == 2 ? bit : 0u;
-              wr3 |= wq == 3 ? bit : 0u;
-            }
-          }
-          s_slot[o + step] = wrote;
-          if (task) trow[i] = task;
+          s_key[o + y] = kx;
+          s_idx[o + y] = ix;
         }
+      } else if (c > kLaneMax) {
+        s_defer[atomicAdd(&s_ndefer, 1u)] = bk << 16;
       }
-    } else {
-      uint32_t maxc = lane_ok ? c : 0;
-#pragma unroll
-      for (int d = 32; d > 0; d >>= 1) {
-        const uint32_t y = __shfl_xor(maxc, d, 64);
-        maxc = y > maxc ? y : maxc;
-      }
-      bool active = lane_ok;
-      for (uint32_t step = 0; step < maxc; step++) {
-        uint64_t src = 0, dst = 0;
-        if (active && step < c) {
-          const uint64_t k = s_key[o + step];
-          const uint64_t i = s_idx[o + step];
-          const uint64_t in = has_in ? G(a.in_scores)[i] : 0;
-          int slot = -1;
-          if (!lane_step<OP>(t, a, b, base, i, k, in, has_in, bsz, src, dst, slot)) {
-            active = false;
-            s_defer[atomicAdd(&s_ndefer, 1u)] = (bk << 16) | step;
-          }
-        }
-        // Accumulations run in batch order: each step's tasks are executed
-        // before the next step reads rows.
-        const uint64_t tm = __ballot(dst != 0);
-        if (dst) {
-          const uint32_t r = __popcll(tm & ((1ull << lane) - 1));
-          s_src[wv][r] = src;
-          s_dst[wv][r] = dst;
-        }
-        __builtin_amdgcn_wave_barrier();
-        if (tm) flush_tasks<U, 2>(__popcll(tm), s_src[wv], s_dst[wv], R, a.value_type);
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-        __builtin_amdgcn_wave_barrier();
-      }
-    }
-    if (lane_ok && bsz != bsz0) G(t.bsize)[b] = bsz;
-    added += (uint32_t)(bsz - bsz0);
-    __syncthreads();
-
-    // 16-lane pass over the buckets handed over: 16 groups per block.
-    const uint32_t nd = s_ndefer;
-    const uint32_t gl = tid & 15;
-    for (uint32_t q = tid >> 4; q < nd; q += kBlock / 16) {
-      const uint32_t v = s_defer[q];
-      const uint32_t l2 = v >> 16, st = v & 0xFFFFu;
-      const uint32_t c2 = s_cnt[l2], o2 = s_off[l2];
-      const uint64_t b2 = part_b0 + l2;
+      const uint64_t base = b * (uint64_t)B;
+      int32_t bsz = lane_ok ? G(t.bsize)[b] : 0;
+      const int32_t bsz0 = bsz;
+      uint32_t wr0 = 0, wr1 = 0, wr2 = 0, wr3 = 0;
       if constexpr (kDeferRows) {
-        // Row tasks the lane pass recorded for this bucket, in batch order.
-        for (uint32_t x = 0; x < st; x++) {
-          const uint64_t i = s_idx[o2 + x];
-          const uint64_t tv = trow[i];
-          if (tv == 0) continue;
-          const uint64_t kind = tv & ~kTaskMask, val = tv & kTaskMask;
-          gptr<const uint8_t> src;
-          gptr<uint8_t> dst;
-          if (kind == kTaskIn) {
-            src = G(a.in_values) + i * (uint64_t)R;
-            dst = G<uint8_t>((uintptr_t)val);
-          } else if (kind == kTaskOut) {
-            src = G<const uint8_t>((uintptr_t)val);
-            dst = G(a.io_values) + i * (uint64_t)R;
-          } else {
-            src = G(a.io_values) + val * (uint64_t)R;
-            dst = G(a.io_values) + i * (uint64_t)R;
+        if (lane_ok) {
+          uint32_t* dg = s_dg + bk * kDgStride;
+          const gptr<uint8_t> rows0 = row_ptr(t, b, 0);
+          constexpr bool may_insert = OP != OP_ASSIGN_SCORES;
+          for (uint32_t step = 0; step < c; step++) {
+            const uint64_t k = s_key[o + step];
+            const uint64_t i = s_idx[o + step];
+            const uint64_t in = has_in ? G(a.in_scores)[i] : 0;
+            const uint64_t h = murmur3(k);
+            const uint32_t start = (uint32_t)(global_idx(t, h) & (B - 1));
+            const uint32_t d = key_digest(h);
+            int dup = 0;
+            const int slot =
+                probe_upsert_lds(t, dg, base, start, d, k, may_insert && bsz < (int32_t)B, &dup);
+            if (slot < 0 && may_insert) {
+              // Eviction path: the 16-lane pass resumes here, after running the
+              // row tasks recorded so far for this bucket.
+              s_defer[atomicAdd(&s_ndefer, 1u)] = (bk << 16) | step;
+              break;
+            }
+            uint64_t src = 0, dst = 0;
+            uint32_t res = 0;
+            if (slot >= 0) {
+              res = lane_apply<OP>(t, a, base, rows0, slot, dup, i, k, in, has_in, d, bsz, src,
+                                   dst);
+              if (res & kLaneDigest) reinterpret_cast<uint8_t*>(dg)[slot] = (uint8_t)d;
+            }
+            uint64_t task = 0;
+            uint8_t wrote = kNoSlot;
+            if (dst) {
+              const uint32_t sl = (uint32_t)slot;
+              const uint32_t bit = 1u << (sl & 31), wq = sl >> 5;
+              const uint32_t cur = wq == 0 ? wr0 : wq == 1 ? wr1 : wq == 2 ? wr2 : wr3;
+              // Latest earlier step of this bucket that wrote the row of `slot`.
+              uint32_t prev = kNone;
+              if (cur & bit)
+                for (uint32_t x = 0; x < step; x++)
+                  if (s_slot[o + x] == (uint8_t)sl) prev = x;
+              if (res & kLaneRead) {
+                // A hit: read the row, or the input of the key that wrote it.
+                task = prev != kNone ? (kTaskFwd | s_idx[o + prev])
+                                     : (kTaskOut | (src & kTaskMask));
+              } else {
+                // The row is written: a later write of the same row supersedes.
+                if (prev != kNone) {
+                  trow[s_idx[o + prev]] = 0;
+                  s_slot[o + prev] = kNoSlot;
+                }
+                task = kTaskIn | (dst & kTaskMask);
+                wrote = (uint8_t)sl;
+                wr0 |= wq == 0 ? bit : 0u;
+                wr1 |= wq == 1 ? bit : 0u;
+                wr2 |= wq == 2 ? bit : 0u;
+                wr3 |= wq == 3 ? bit : 0u;
+              }
+            }
+            s_slot[o + step] = wrote;
+            if (task) trow[i] = task;
           }
-          copy_units<U>(dst, src, R, gl, 16);
-          if (gl == 0) trow[i] = 0;
         }
-      }
-      Bucket16 S;
-      bucket_load(t, S, b2, gl);
-      if (c2 <= kLaneMax) {
-        for (uint32_t step = st; step < c2; step++)
-          apply_key<OP, U>(t, S, a, s_idx[o2 + step], s_key[o2 + step]);
       } else {
-        // Long run, not sorted: take the entries by increasing batch index.
-        uint32_t last = 0;  // batch index + 1 of the previous key
-        for (uint32_t step = 0; step < c2; step++) {
-          uint32_t mi = kNone, mp = 0;
-          for (uint32_t x = gl; x < c2; x += 16) {
-            const uint32_t iv = s_idx[o2 + x] + 1u;
-            if (iv > last && iv < mi) {
-              mi = iv;
-              mp = x;
-            }
-          }
+        uint32_t maxc = lane_ok ? c : 0;
 #pragma unroll
-          for (int d = 8; d > 0; d >>= 1) {
-            const uint32_t om = __shfl_xor(mi, d, 16);
-            const uint32_t op = __shfl_xor(mp, d, 16);
-            if (om < mi) {
-              mi = om;
-              mp = op;
+        for (int d = 32; d > 0; d >>= 1) {
+          const uint32_t y = __shfl_xor(maxc, d, 64);
+          maxc = y > maxc ? y : maxc;
+        }
+        bool active = lane_ok;
+        for (uint32_t step = 0; step < maxc; step++) {
+          uint64_t src = 0, dst = 0;
+          if (active && step < c) {
+            const uint64_t k = s_key[o + step];
+            const uint64_t i = s_idx[o + step];
+            const uint64_t in = has_in ? G(a.in_scores)[i] : 0;
+            int slot = -1;
+            if (!lane_step<OP>(t, a, b, base, i, k, in, has_in, bsz, src, dst, slot)) {
+              active = false;
+              s_defer[atomicAdd(&s_ndefer, 1u)] = (bk << 16) | step;
             }
           }
-          last = mi;
-          apply_key<OP, U>(t, S, a, (uint64_t)(mi - 1), s_key[o2 + mp]);
+          // Accumulations run in batch order: each step's tasks are executed
+          // before the next step reads rows.
+          const uint64_t tm = __ballot(dst != 0);
+          if (dst) {
+            const uint32_t r = __popcll(tm & ((1ull << lane) - 1));
+            s_src[wv][r] = src;
+            s_dst[wv][r] = dst;
+          }
+          __builtin_amdgcn_wave_barrier();
+          if (tm) flush_tasks<U, 2>(__popcll(tm), s_src[wv], s_dst[wv], R, a.value_type);
+          __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+          __builtin_amdgcn_wave_barrier();
         }
       }
-      bucket_finish(t, S);
-    }
-    __syncthreads();
-    if (kDeferRows) {
-      // The row tasks of this run, executed before another run can touch
-      // the same slots.
-      for (uint32_t e0 = 0; e0 < mc; e0 += kBlock) {
-        const uint32_t e = e0 + tid;
-        wave_run_tasks<U>(a, trow, e < mc ? s_idx[e] : 0, e < mc, R, s_rows[wv]);
+      if (lane_ok && bsz != bsz0) G(t.bsize)[b] = bsz;
+      added += (uint32_t)(bsz - bsz0);
+      __syncthreads();
+
+      // 16-lane pass over the buckets handed over: 16 groups per block.
+      const uint32_t nd = s_ndefer;
+      const uint32_t gl = tid & 15;
+      for (uint32_t q = tid >> 4; q < nd; q += kBlock / 16) {
+        const uint32_t v = s_defer[q];
+        const uint32_t l2 = v >> 16, st = v & 0xFFFFu;
+        const uint32_t c2 = s_cnt[l2], o2 = s_off[l2];
+        const uint64_t b2 = part_b0 + l2;
+        if constexpr (kDeferRows) {
+          // Row tasks the lane pass recorded for this bucket, in batch order.
+          for (uint32_t x = 0; x < st; x++) {
+            const uint64_t i = s_idx[o2 + x];
+            const uint64_t tv = trow[i];
+            if (tv == 0) continue;
+            const uint64_t kind = tv & ~kTaskMask, val = tv & kTaskMask;
+            gptr<const uint8_t> src;
+            gptr<uint8_t> dst;
+            if (kind == kTaskIn) {
+              src = G(a.in_values) + i * (uint64_t)R;
+              dst = G<uint8_t>((uintptr_t)val);
+            } else if (kind == kTaskOut) {
+              src = G<const uint8_t>((uintptr_t)val);
+              dst = G(a.io_values) + i * (uint64_t)R;
+            } else {
+              src = G(a.io_values) + val * (uint64_t)R;
+              dst = G(a.io_values) + i * (uint64_t)R;
+            }
+            copy_units<U>(dst, src, R, gl, 16);
+            if (gl == 0) trow[i] = 0;
+          }
+        }
+        Bucket16 S;
+        bucket_load(t, S, b2, gl);
+        if (c2 <= kLaneMax) {
+          for (uint32_t step = st; step < c2; step++)
+            apply_key<OP, U>(t, S, a, s_idx[o2 + step], s_key[o2 + step]);
+        } else {
+          // Long run, not sorted: take the entries by increasing batch index.
+          uint32_t last = 0;  // batch index + 1 of the previous key
+          for (uint32_t step = 0; step < c2; step++) {
+            uint32_t mi = kNone, mp = 0;
+            for (uint32_t x = gl; x < c2; x += 16) {
+              const uint32_t iv = s_idx[o2 + x] + 1u;
+              if (iv > last && iv < mi) {
+                mi = iv;
+                mp = x;
+              }
+            }
+#pragma unroll
+            for (int d = 8; d > 0; d >>= 1) {
+              const uint32_t om = __shfl_xor(mi, d, 16);
+              const uint32_t op = __shfl_xor(mp, d, 16);
+              if (om < mi) {
+                mi = om;
+                mp = op;
+              }
+            }
+            last = mi;
+            apply_key<OP, U>(t, S, a, (uint64_t)(mi - 1), s_key[o2 + mp]);
+          }
+        }
+        bucket_finish(t, S);
       }
       __syncthreads();
+      if (kDeferRows) {
+        // The row tasks of this run, executed before another run can touch
+        // the same slots.
+        for (uint32_t e0 = 0; e0 < mc; e0 += kBlock) {
+          const uint32_t e = e0 + tid;
+          wave_run_tasks<U>(a, trow, e < mc ? s_idx[e] : 0, e < mc, R, s_rows[wv]);
+        }
+        __syncthreads();
+      }
+      c0 = c1;
     }
-    c0 = c1;
+    __syncthreads();  // LDS is reused by the next partition
   }
 #pragma unroll
   for (int d = 32; d > 0; d >>= 1) added += __shfl_xor(added, d, 64);
@@ -1644,7 +1678,7 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
 
 // Single-run apply of a partition whose entries fit one LDS load (kFastLds)
 // and whose buckets receive at most kLaneMax keys each (every partition, for
-// uniform keys); other partitions are left to k_apply_part (pflag[p] = 0).
+// uniform keys); other partitions are listed for k_apply_part.
 //
 // The batch-order semantics (keys applied one at a time in increasing batch
 // index, each by the reference's per-key algorithm) are reproduced with the
@@ -1823,13 +1857,10 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
   const uint32_t p = blockIdx.x;
   const uint32_t base_e = ps.pinfo[2 * p], m = ps.pinfo[2 * p + 1];
   if (m > kFastLds) {
-    if (tid == 0) ps.pflag[p] = 0;
+    if (tid == 0) ps.plist[atomicAdd(&ps.dctr[2], 1u)] = p;  // k_apply_part takes it
     return;
   }
-  if (m == 0) {
-    if (tid == 0) ps.pflag[p] = 1;
-    return;
-  }
+  if (m == 0) return;
   const uint32_t B = t.B;
   const uint32_t R = t.row_bytes;
   const uint64_t part_b0 = (uint64_t)p * kPartBuckets;
@@ -1882,10 +1913,10 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
     if (tid == 0) s_off[kPartBuckets] = m;
     lds_barrier();
     if (s_big) {
-      if (tid == 0) ps.pflag[p] = 0;  // a long bucket: k_apply_part orders it
+      // A long bucket: k_apply_part orders it.
+      if (tid == 0) ps.plist[atomicAdd(&ps.dctr[2], 1u)] = p;
       return;
     }
-    if (tid == 0) ps.pflag[p] = 1;
 #pragma unroll
     for (uint32_t q = 0; q < kPer; q++) {
       if (tid + q * kBlock < m) {
@@ -2565,13 +2596,16 @@ static void apply_part_op(const TableView& t, const ApplyArgs& a, const PartScra
   hipLaunchKernelGGL(k_pscatter, dim3(ps.chunks), dim3(kBlock), lds, s, t, a.keys, a.n, ps);
   const dim3 g(ps.np), b(kBlock);
   constexpr bool fast = OP != OP_ACCUM_OR_ASSIGN;
-  const dim3 gd(grid_for(a.n * 16, kBlock, 4096));
+  // After the single-run kernel, the eviction path and the multi-run kernel
+  // walk device-side lists that are usually empty: small grids.
+  const dim3 gd(grid_for(a.n * 16, kBlock, 2048));
+  const dim3 gp(fast ? (ps.np < 256 ? ps.np : 256) : ps.np);
 #define HKV_PART_U(UU)                                                                       \
   if constexpr (fast) {                                                                      \
     hipLaunchKernelGGL((k_apply_fast<fast ? OP : 0, UU>), g, b, 0, s, t, a, ps);             \
     hipLaunchKernelGGL((k_apply_deferred<fast ? OP : 0, UU>), gd, b, 0, s, t, a, ps);        \
   }                                                                                          \
-  hipLaunchKernelGGL((k_apply_part<OP, UU>), g, b, 0, s, t, a, ps, fast ? 0 : 1)
+  hipLaunchKernelGGL((k_apply_part<OP, UU>), gp, b, 0, s, t, a, ps, fast ? 0 : 1)
   switch (a.unit) {
     case 16: HKV_PART_U(16); break;
     case 8: HKV_PART_U(8); break;

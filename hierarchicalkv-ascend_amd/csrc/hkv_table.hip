@@ -120,8 +120,8 @@ struct hkv_table {
   uint32_t* p_spill = nullptr;
   uint64_t* p_trow = nullptr;  // zero between calls
   uint64_t p_trow_cap = 0;
-  uint32_t* p_flag = nullptr;
-  uint64_t p_flag_cap = 0;
+  uint32_t* p_list = nullptr;  // partitions left to the multi-run kernel
+  uint64_t p_list_cap = 0;
   uint32_t* p_drec = nullptr;
   uint64_t* p_dpool = nullptr;
   uint64_t p_defer_cap = 0;
@@ -217,7 +217,7 @@ struct hkv_table {
     (void)hipFree(p_info);
     (void)hipFree(p_spill);
     (void)hipFree(p_trow);
-    (void)hipFree(p_flag);
+    (void)hipFree(p_list);
     (void)hipFree(p_drec);
     (void)hipFree(p_dpool);
     (void)hipFree(p_dctr);
@@ -283,10 +283,10 @@ struct hkv_table {
       launch_fill_u64(p_trow, 0, n, s);
       p_trow_cap = n;
     }
-    if (np > p_flag_cap) {
-      if (p_flag) hip_check(hipFree(p_flag), "hipFree");
-      hip_check(hipMalloc(&p_flag, np * sizeof(uint32_t)), "hipMalloc(part flags)");
-      p_flag_cap = np;
+    if (np > p_list_cap) {
+      if (p_list) hip_check(hipFree(p_list), "hipFree");
+      hip_check(hipMalloc(&p_list, np * sizeof(uint32_t)), "hipMalloc(part list)");
+      p_list_cap = np;
     }
     if (n > p_defer_cap) {
       if (p_drec) hip_check(hipFree(p_drec), "hipFree");
@@ -295,8 +295,8 @@ struct hkv_table {
       hip_check(hipMalloc(&p_dpool, n * 16), "hipMalloc(defer pool)");
       p_defer_cap = n;
     }
-    if (!p_dctr) hip_check(hipMalloc(&p_dctr, 2 * sizeof(uint32_t)), "hipMalloc(defer counts)");
-    *ps = PartScratch{p_hist, p_ent,  p_info,  p_spill,      p_trow,       p_flag,
+    if (!p_dctr) hip_check(hipMalloc(&p_dctr, 4 * sizeof(uint32_t)), "hipMalloc(part counters)");
+    *ps = PartScratch{p_hist, p_ent,  p_info,  p_spill,      p_trow,       p_list,
                       p_drec, p_dpool, p_dctr, (uint32_t)np, (uint32_t)ng, (uint32_t)cap};
     return true;
   }
