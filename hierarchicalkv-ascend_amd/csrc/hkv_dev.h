@@ -255,7 +255,8 @@ template <> struct UnitT<2> { using T = uint16_t; };
 template <> struct UnitT<1> { using T = uint8_t; };
 
 // `nl` lanes (rank `r` among them) copy `bytes` from src to dst in U-byte
-// units.
+// units.  Rows are streamed (non-temporal loads and stores), which keeps the
+// bucket metadata in the L2 cache.
 template <int U>
 __device__ __forceinline__ void copy_units(gptr<uint8_t> dst, gptr<const uint8_t> src,
                                            uint32_t bytes, uint32_t r, uint32_t nl) {
@@ -265,13 +266,15 @@ __device__ __forceinline__ void copy_units(gptr<uint8_t> dst, gptr<const uint8_t
   gptr<const T> s = (gptr<const T>)src;
   uint32_t u = r;
   for (; u + 3 * nl < units; u += 4 * nl) {
-    const T a = s[u], b = s[u + nl], c = s[u + 2 * nl], e = s[u + 3 * nl];
-    d[u] = a;
-    d[u + nl] = b;
-    d[u + 2 * nl] = c;
-    d[u + 3 * nl] = e;
+    const T a = __builtin_nontemporal_load(&s[u]), b = __builtin_nontemporal_load(&s[u + nl]),
+            c = __builtin_nontemporal_load(&s[u + 2 * nl]),
+            e = __builtin_nontemporal_load(&s[u + 3 * nl]);
+    __builtin_nontemporal_store(a, &d[u]);
+    __builtin_nontemporal_store(b, &d[u + nl]);
+    __builtin_nontemporal_store(c, &d[u + 2 * nl]);
+    __builtin_nontemporal_store(e, &d[u + 3 * nl]);
   }
-  for (; u < units; u += nl) d[u] = s[u];
+  for (; u < units; u += nl) __builtin_nontemporal_store(__builtin_nontemporal_load(&s[u]), &d[u]);
 }
 
 __device__ __forceinline__ void copy_row(gptr<uint8_t> dst, gptr<const uint8_t> src,

@@ -364,17 +364,36 @@ __global__ __launch_bounds__(kBlock) void k_route(TableView t, const uint64_t* _
 enum Outcome : uint32_t { R_DUP = 1, R_EMPTY = 2, R_RECLAIMED = 3, R_EVICT = 4, R_REFUSED = 5 };
 
 // State of one bucket held by a 16-lane group: lane l owns slots l + 16*j
-// (j = 0..7).  Only the owner lane ever reads or writes a slot's key, score
-// and digest, so the slots need no register cache: the owner re-reads them
-// (same-thread ordering makes its own earlier writes visible).  The eight
-// digests of a lane are kept packed in two words.
+// (j = 0..7) and keeps their digests (packed in two words), keys and scores
+// in registers for as long as the group applies keys to the bucket, so an
+// evicting key scans no memory.  Only the owner lane reads or writes a slot,
+// which keeps the registers current; writes go through to the table.
 struct Bucket16 {
   uint64_t b;
   uint64_t base;  // b * B
   uint32_t l;
   uint32_t dg0, dg1;  // digest of slot l+16j in byte j (dg0: j<4, dg1: j>=4)
   int32_t bsz, bsz0;
+  uint64_t key[8], score[8];  // record of slot l+16j
 };
+
+// Element j of a lane's eight records (j is not a compile-time constant).
+// Written as mask arithmetic: a chain of selects would be turned into an
+// indexed stack array.
+__device__ __forceinline__ uint64_t rec_get(const uint64_t (&v)[8], uint32_t j) {
+  uint64_t r = 0;
+#pragma unroll
+  for (uint32_t q = 0; q < 8; q++) r |= v[q] & (0ull - (uint64_t)(j == q));
+  return r;
+}
+
+__device__ __forceinline__ void rec_set(uint64_t (&v)[8], uint32_t j, uint64_t x) {
+#pragma unroll
+  for (uint32_t q = 0; q < 8; q++) {
+    const uint64_t m = 0ull - (uint64_t)(j == q);
+    v[q] = (v[q] & ~m) | (x & m);
+  }
+}
 
 __device__ __forceinline__ uint32_t dg_of(const Bucket16& S, uint32_t j) {
   return ((j < 4 ? S.dg0 : S.dg1) >> (8 * (j & 3))) & 0xFFu;
@@ -397,6 +416,12 @@ __device__ __forceinline__ void bucket_load(const TableView& t, Bucket16& S, uin
           ((uint32_t)dg[48] << 24);
   S.dg1 = (uint32_t)dg[64] | ((uint32_t)dg[80] << 8) | ((uint32_t)dg[96] << 16) |
           ((uint32_t)dg[112] << 24);
+#pragma unroll
+  for (uint32_t j = 0; j < 8; j++) {
+    const u64x2 r = slot_load(t, S.base + l + 16 * j);
+    S.key[j] = r.x;
+    S.score[j] = r.y;
+  }
   S.bsz = S.bsz0 = G(t.bsize)[b];
 }
 
@@ -464,7 +489,7 @@ __device__ __forceinline__ void apply_key(const TableView& t, Bucket16& S, const
   uint32_t best = kNone;
 #pragma unroll
   for (int j = 0; j < SPL; j++) {
-    if (dg_of(S, j) == d && slot_key(t, S.base + l + 16 * j) == k) {
+    if (dg_of(S, j) == d && S.key[j] == k) {
       const uint32_t p = l + 16 * j;
       const uint32_t rk = (((p - a4) & (B - 1)) << 8) | p;
       best = rk < best ? rk : best;
@@ -504,9 +529,8 @@ __device__ __forceinline__ void apply_key(const TableView& t, Bucket16& S, const
 #pragma unroll
       for (int j = 0; j < SPL; j++) {
         const uint32_t p = l + 16 * j;
-        const u64x2 rec = slot_load(t, S.base + p);
-        const uint64_t kj = rec.x;
-        const uint64_t sj = rec.y;
+        const uint64_t kj = S.key[j];
+        const uint64_t sj = S.score[j];
         uint32_t rank;
         bool elig;
         if (a.rule == RULE_DIGEST16) {
@@ -533,7 +557,7 @@ __device__ __forceinline__ void apply_key(const TableView& t, Bucket16& S, const
         // Every eligible score is MAX_SCORE: the start slot is taken.
         mp = start;
         uint64_t kk = 0;
-        if (l == (start & 15u)) kk = slot_key(t, S.base + start);
+        if (l == (start & 15u)) kk = rec_get(S.key, start >> 4);
         mk = shfl_u64(kk, (int)(start & 15u), 16);
       }
       if (des < ms) {
@@ -597,9 +621,9 @@ __device__ __forceinline__ void apply_key(const TableView& t, Bucket16& S, const
   if (l == owner) {
     uint64_t old = 0;
     if (res == R_DUP && (a.sc.strategy == kLfu || a.sc.strategy == kEpochLfu))
-      old = slot_score(t, S.base + pos);
+      old = rec_get(S.score, jj);
     else if (res != R_DUP && a.sc.strategy == kLfu && !has_in)
-      old = slot_score(t, S.base + pos);
+      old = rec_get(S.score, jj);
     bool w;
     uint64_t ns;
     if (OP == OP_ASSIGN_SCORES) {
@@ -610,13 +634,19 @@ __device__ __forceinline__ void apply_key(const TableView& t, Bucket16& S, const
       ns = score_new(a.sc, has_in, in, des, old, &w);
     }
     if (res == R_DUP) {
-      if (w) slot_score(t, S.base + pos) = ns;
+      if (w) {
+        slot_score(t, S.base + pos) = ns;
+        rec_set(S.score, jj, ns);
+      }
     } else if (w) {
       slot_store(t, S.base + pos, k, ns);
       G(t.digests)[S.base + pos] = (uint8_t)d;
       dg_set(S, jj, d);
+      rec_set(S.key, jj, k);
+      rec_set(S.score, jj, ns);
     } else {
       slot_key(t, S.base + pos) = k;
+      rec_set(S.key, jj, k);
     }
   }
 }
@@ -2071,6 +2101,12 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
       const uint64_t h = murmur3(k);
       const uint32_t start = (uint32_t)(global_idx(t, h) & (B - 1));
       const uint32_t d = key_digest(h);
+      if (may_insert && bsz >= B) {
+        // A full bucket: the eviction path (which also finds a present key)
+        // takes the rest of it, without a scan of the whole bucket here.
+        stop = r;
+        break;
+      }
       int dup = 0;
       const int sl = probe_serial(t, base, f0, f1, f2, f3, s_key, s_slot, s_fl, s_rank, lo, hi, r,
                                   start, d, k, !may_insert || bsz < B, &dup);
