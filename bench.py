@@ -29,6 +29,15 @@ DIM = 64
 BATCH = 1 << 20
 
 
+# HBM bytes per key that each operation's kernels move at this workload, from
+# rocprofv3 FETCH_SIZE and WRITE_SIZE passes over
+# `bench.py --no-cpu-baseline --no-extra --steps 4 --warmup 1 --calibrate`,
+# scaled by the factors a plain 1 GiB device copy gives in the same run
+# (fetch x2.0, write x1.0); the per-kernel figures are in
+# profiles/insert_or_assign_find_cap64M_dim64_hbm_bytes.md.
+MEASURED_BYTES_PER_KEY = {"insert_new": 737.6, "find_hit": 661.7}
+
+
 def algo_bytes(op, dim=DIM):
     """Algorithmic bytes per key (fixed model: S per random metadata touch,
     x2 when read-modify-write; V = 4*dim per row direction)."""
@@ -247,16 +256,20 @@ def main():
 
     # The dominant operation of the step sets the roofline line.
     if ins_ms >= find_ms:
-        roof = {"kernel": "insert_or_assign (route + apply kernels)",
+        roof = {"kernel": "insert_or_assign (k_pcount + k_pscan + k_pscatter + "
+                          "k_apply_fast + k_apply_deferred + k_apply_part)",
                 "achieved": round(ins_gbs, 1), "bytes_per_key": algo_bytes("insert_new"),
-                "ms_per_launch": round(ins_ms, 4)}
+                "ms_per_launch": round(ins_ms, 4), "op": "insert_new"}
     else:
-        roof = {"kernel": "find", "achieved": round(find_gbs, 1),
+        roof = {"kernel": "find (k_find)", "achieved": round(find_gbs, 1),
                 "bytes_per_key": algo_bytes("find_hit"),
-                "ms_per_launch": round(find_ms, 4)}
+                "ms_per_launch": round(find_ms, 4), "op": "find_hit"}
+    traffic = round(MEASURED_BYTES_PER_KEY[roof["op"]] * BATCH)
     roofline = {"bound": "hbm", "achieved": roof["achieved"], "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(roof["achieved"] / HBM_PEAK_GBS, 4),
-                "traffic": None, "kernel": roof["kernel"],
+                "traffic": traffic, "traffic_unit": "bytes per launch (rocprofv3 "
+                "FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
+                "kernel": roof["kernel"],
                 "keys_per_launch": BATCH, "bytes_per_key": roof["bytes_per_key"],
                 "ms_per_launch": roof["ms_per_launch"]}
 
