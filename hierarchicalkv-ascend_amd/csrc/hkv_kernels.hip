@@ -1753,70 +1753,88 @@ __device__ __forceinline__ uint32_t sel4(uint32_t w0, uint32_t w1, uint32_t w2, 
   return q == 0 ? w0 : q == 1 ? w1 : q == 2 ? w2 : w3;
 }
 
-// Probe of one key over the two 16-slot digest chunks w0 (the chunk of
-// start's group) and w1 (the next one, circularly), in the order of
-// find_without_lock / insert_or_assign_kernel.h:105-183: 4-slot groups from
-// start's group; in each group first the digest matches, then the EMPTY
-// slots (in the first group only at or after start).
+// Probe of one key in the order of find_without_lock /
+// insert_or_assign_kernel.h:105-183: 4-slot groups from start's group,
+// circularly; in each group first the digest matches, then the EMPTY slots
+// (in the first group only at or after start).  The first two digest matches
+// met before the probe ends are recorded: their keys decide whether the key
+// is present.  A probe the window does not decide goes to the serial lane.
 struct WinProbe {
   uint32_t slot;    // first EMPTY slot of the probe (when found)
-  uint32_t c0, c1;  // first two digest matches met up to that group (kNone: none)
-  bool found;       // the probe reached an EMPTY slot inside the window
+  uint32_t c0, c1;  // first two digest matches (kNone: none)
+  uint32_t slot2;   // the next EMPTY slot after `slot` with no digest match
+                    // between them (kNone: none in the window)
+  bool found;       // the probe reached an EMPTY slot
   bool over;        // more than two digest matches
+  bool done;        // `slot2` is decided
 };
 
+// One group (digests w, first slot gs) of a probe.  After the first EMPTY
+// slot the scan goes on for the second one: if an earlier key of the call
+// takes the first, the key's probe ends at the second unless a digest match
+// lies between them.
+__device__ __forceinline__ void probe_group(WinProbe& r, uint32_t w, uint32_t gs, uint32_t rep,
+                                            uint32_t emask) {
+  uint32_t m = eq_bytes4(w, rep);
+  uint32_t e = eq_bytes4(w, (uint32_t)kEmptyDigest * 0x01010101u) & emask;
+  if (r.found) {
+    if (m) r.done = true;
+    else if (e) {
+      r.slot2 = gs + __builtin_ctz(e);
+      r.done = true;
+    }
+    return;
+  }
+  while (m) {
+    const uint32_t p = gs + __builtin_ctz(m);
+    m &= m - 1;
+    if (r.c0 == kNone) r.c0 = p;
+    else if (r.c1 == kNone) r.c1 = p;
+    else r.over = true;
+  }
+  if (e) {
+    r.found = true;
+    r.slot = gs + __builtin_ctz(e);
+    e &= e - 1;  // later EMPTY slots of the same group (its matches are recorded)
+    if (e) {
+      r.slot2 = gs + __builtin_ctz(e);
+      r.done = true;
+    }
+  }
+}
+
+// The probe over its first two 16-slot digest chunks: w0 (the chunk of
+// start's group) and w1 (the next one, circularly).  `empties` = false scans
+// for the key only (a full bucket).
 __device__ __forceinline__ WinProbe probe_window(u32x4 w0, u32x4 w1, uint32_t start, uint32_t d,
-                                                 uint32_t B) {
+                                                 uint32_t B, bool empties) {
   const uint32_t a = start & ~3u;
   const uint32_t cbase = a & ~15u;    // first slot of chunk w0
   const uint32_t g0 = (a >> 2) & 3u;  // start's group inside w0
   const uint32_t rep = d * 0x01010101u;
-  const uint32_t erep = (uint32_t)kEmptyDigest * 0x01010101u;
-  const uint32_t first_mask = ~((1u << (start - a)) - 1u) & 0xFu;
+  const uint32_t emask = empties ? 0xFu : 0u;
+  const uint32_t first_mask = ~((1u << (start - a)) - 1u) & emask;
   const uint32_t words[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-  WinProbe r{0, kNone, kNone, false, false};
+  WinProbe r{0, kNone, kNone, kNone, false, false, false};
 #pragma unroll
   for (uint32_t q = 0; q < 8; q++) {
-    if (q < g0 || r.found) continue;
-    const uint32_t gs = (cbase + 4 * q) & (B - 1);  // first slot of the group
-    uint32_t m = eq_bytes4(words[q], rep);
-    while (m) {
-      const uint32_t p = gs + __builtin_ctz(m);
-      m &= m - 1;
-      if (r.c0 == kNone) r.c0 = p;
-      else if (r.c1 == kNone) r.c1 = p;
-      else r.over = true;
-    }
-    uint32_t e = eq_bytes4(words[q], erep);
-    if (q == g0) e &= first_mask;
-    if (e) {
-      r.found = true;
-      r.slot = gs + __builtin_ctz(e);
-    }
+    if (q < g0 || r.done) continue;
+    probe_group(r, words[q], (cbase + 4 * q) & (B - 1), rep, q == g0 ? first_mask : emask);
   }
   return r;
 }
 
-// Entry x < hi of the bucket (entries [lo, hi)) with rank r.
-__device__ __forceinline__ uint32_t entry_of_rank(const uint8_t* s_rank, uint32_t lo, uint32_t hi,
-                                                  uint32_t r) {
-  uint32_t e = lo;
-  for (uint32_t x = lo; x < hi; x++)
-    if (s_rank[x] == r) e = x;
-  return e;
-}
-
 // Probe of key k for the serial lane, over the bucket's digests in memory.
 // Slots filled by the call's earlier keys (bit set in f0..f3) show the empty
-// digest in memory; their keys are those of the entries of rank < r whose
-// outcome took the slot.  Returns the slot holding k (*dup = 1), else the
+// digest in memory; their keys are those of the entries [lo, e) (the earlier
+// keys of the bucket, in batch order) whose outcome took the slot.  Returns the slot holding k (*dup = 1), else the
 // first EMPTY slot when `empties` (*dup = 0), else -1.
 __device__ __forceinline__ int probe_serial(const TableView& t, uint64_t base, uint32_t f0,
                                             uint32_t f1, uint32_t f2, uint32_t f3,
                                             const uint64_t* s_key, const uint8_t* s_slot,
-                                            const uint8_t* s_fl, const uint8_t* s_rank,
-                                            uint32_t lo, uint32_t hi, uint32_t r, uint32_t start,
-                                            uint32_t d, uint64_t k, bool empties, int* dup) {
+                                            const uint8_t* s_fl, uint32_t lo, uint32_t e,
+                                            uint32_t start, uint32_t d, uint64_t k, bool empties,
+                                            int* dup) {
   const uint32_t B = t.B;
   gptr<const u32x4> drow = (gptr<const u32x4>)(G(t.digests) + base);
   const uint32_t a = start & ~3u;
@@ -1846,19 +1864,18 @@ __device__ __forceinline__ int probe_serial(const TableView& t, uint64_t base, u
     while (fq) {
       const uint32_t p = g + __builtin_ctz(fq);
       fq &= fq - 1;
-      for (uint32_t x = lo; x < hi; x++)
-        if (s_rank[x] < r && s_slot[x] == p && (s_fl[x] & kResMask) == kResNew &&
-            s_key[x] == k) {
+      for (uint32_t x = lo; x < e; x++)
+        if (s_slot[x] == p && (s_fl[x] & kResMask) == kResNew && s_key[x] == k) {
           *dup = 1;
           return (int)p;
         }
     }
     if (!empties) continue;
-    uint32_t e = eq_bytes4(w, erep) & ~fm;
-    if (off == 0) e &= ~((1u << (start - a)) - 1u);
-    if (e) {
+    uint32_t em = eq_bytes4(w, erep) & ~fm;
+    if (off == 0) em &= ~((1u << (start - a)) - 1u);
+    if (em) {
       *dup = 0;
-      return (int)(g + __builtin_ctz(e));
+      return (int)(g + __builtin_ctz(em));
     }
   }
   return -1;
@@ -1871,18 +1888,26 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
   constexpr bool may_insert = OP != OP_ASSIGN_SCORES;
   constexpr bool moves_rows = OP != OP_ASSIGN_SCORES;
   constexpr bool reads_rows = OP == OP_FIND_OR_INSERT;
+  // Entries of the partition, grouped by bucket and in batch order inside a
+  // bucket: the rank of entry e of bucket [lo, hi) in the batch is e - lo.
   __shared__ uint64_t s_key[kFastLds];
   __shared__ uint64_t s_sc[kFastLds];     // input score, then the score of the record
   __shared__ uint32_t s_idx[kFastLds];    // batch index
   __shared__ uint8_t s_slot[kFastLds];    // slot of the outcome (kNoSlot: none)
   __shared__ uint8_t s_fl[kFastLds];      // outcome, metadata record and row task
-  __shared__ uint8_t s_rank[kFastLds];    // batch order inside the bucket
+  __shared__ uint8_t s_slot2[kFastLds];   // second EMPTY slot of the probe (kNoSlot: none)
   __shared__ uint32_t s_cnt[kPartBuckets];  // keys per bucket, fill pointers, then stops
   __shared__ uint32_t s_off[kPartBuckets + 1];  // first entry of each bucket
   __shared__ uint8_t s_bsz[kPartBuckets];   // bucket sizes before the call
-  __shared__ uint32_t s_rows[kBlock / 64][64];
+  static_assert(sizeof(uint64_t) * kFastLds >= sizeof(uint32_t) * kBlock, "row lists");
+  // Row lists of the copies, in the score array (no longer read by then).
+  uint32_t(*s_rows)[64] = reinterpret_cast<uint32_t(*)[64]>(s_sc);
   __shared__ uint32_t s_wsum[kBlock / 64];
   __shared__ uint32_t s_big;
+  __shared__ uint32_t s_nrec, s_npool;  // hand-over records and pool entries of the block
+  __shared__ uint8_t s_serial[kPartBuckets];  // buckets left to the serial lanes
+  __shared__ uint32_t s_nser;
+  __shared__ uint32_t s_rbase, s_pbase;
   const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const uint32_t p = blockIdx.x;
   const uint32_t base_e = ps.pinfo[2 * p], m = ps.pinfo[2 * p + 1];
@@ -1919,7 +1944,12 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
       lb[q] = (uint32_t)(bucket_of(t, ev[q].x) % kPartBuckets);
     s_cnt[tid] = 0;
     s_bsz[tid] = (uint8_t)bsz_own;
-    if (tid == 0) s_big = 0;
+    if (tid == 0) {
+      s_big = 0;
+      s_nrec = 0;
+      s_npool = 0;
+      s_nser = 0;
+    }
     lds_barrier();
 #pragma unroll
     for (uint32_t q = 0; q < kPer; q++)
@@ -1950,15 +1980,12 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
 #pragma unroll
     for (uint32_t q = 0; q < kPer; q++) {
       if (tid + q * kBlock < m) {
-        pos[q] = atomicAdd(&s_cnt[lb[q]], 1u);
-        s_key[pos[q]] = ev[q].x;
-        s_idx[pos[q]] = (uint32_t)ev[q].y;
-        s_sc[pos[q]] = inq[q];
+        s_idx[atomicAdd(&s_cnt[lb[q]], 1u)] = (uint32_t)ev[q].y;
       }
     }
     lds_barrier();
     s_cnt[tid] = kNone;  // first rank the parallel pass does not apply (none yet)
-    // Rank of each entry in batch order inside its bucket.
+    // Batch order inside each bucket: every entry moves to lo + its rank.
 #pragma unroll
     for (uint32_t q = 0; q < kPer; q++) {
       if (tid + q * kBlock < m) {
@@ -1966,9 +1993,19 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
         const uint32_t iv = (uint32_t)ev[q].y;
         uint32_t r = 0;
         for (uint32_t y = lo; y < hi; y++) r += s_idx[y] < iv ? 1u : 0u;
-        s_rank[pos[q]] = (uint8_t)r;
+        pos[q] = lo + r;
       }
     }
+    lds_barrier();
+#pragma unroll
+    for (uint32_t q = 0; q < kPer; q++) {
+      if (tid + q * kBlock < m) {
+        s_key[pos[q]] = ev[q].x;
+        s_idx[pos[q]] = (uint32_t)ev[q].y;
+        s_sc[pos[q]] = inq[q];
+      }
+    }
+    lds_barrier();
   }
 
   /* B. Outcome of every key on the table before the call, with the score,
@@ -1994,12 +2031,19 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
 #pragma unroll
     for (uint32_t q = 0; q < kPer; q++) {
       const uint32_t e = tid + q * kBlock;
-      k0[q] = k1[q] = 0;
-      wp[q] = WinProbe{0, kNone, kNone, false, true};
+      wp[q] = WinProbe{0, kNone, kNone, kNone, false, true, true};
       if (e < m) {
-        const uint64_t k = s_key[e];
-        const uint32_t d = key_digest(murmur3(k));
-        wp[q] = probe_window(w0[q], w1[q], (uint32_t)(gi[q] & (B - 1)), d, B);
+        const uint32_t d = key_digest(murmur3(s_key[e]));
+        const uint32_t lbk = (uint32_t)((gi[q] >> t.bshift) % kPartBuckets);
+        const bool empties = !may_insert || s_bsz[lbk] < B;
+        wp[q] = probe_window(w0[q], w1[q], (uint32_t)(gi[q] & (B - 1)), d, B, empties);
+      }
+    }
+#pragma unroll
+    for (uint32_t q = 0; q < kPer; q++) {
+      const uint32_t e = tid + q * kBlock;
+      k0[q] = k1[q] = 0;
+      if (e < m) {
         const uint64_t base = (gi[q] >> t.bshift) * B;
         if (wp[q].c0 != kNone) k0[q] = slot_key(t, base + wp[q].c0);
         if (wp[q].c1 != kNone) k1[q] = slot_key(t, base + wp[q].c1);
@@ -2011,15 +2055,13 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
       if (e >= m) continue;
       const uint64_t k = s_key[e];
       const uint64_t in = s_sc[e];
-      const uint32_t lbk = (uint32_t)((gi[q] >> t.bshift) % kPartBuckets);
-      const bool empties = !may_insert || s_bsz[lbk] < B;
       uint8_t fl = kResSlow, slot = kNoSlot;
       uint64_t sc = 0;
       // A verified digest match is the first one in probe order, so the key
       // is present there whether or not the window reached an EMPTY slot.
       const bool hit0 = wp[q].c0 != kNone && k0[q] == k;
       const bool hit1 = !hit0 && wp[q].c1 != kNone && k1[q] == k;
-      if (hit0 || hit1 || (wp[q].found && !wp[q].over && empties)) {
+      if (hit0 || hit1 || (wp[q].found && !wp[q].over)) {
         const uint64_t des = score_desired(a.sc, has_in, in);
         bool w;
         if (hit0 || hit1) {
@@ -2041,6 +2083,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
         }
       }
       s_slot[e] = slot;
+      s_slot2[e] = wp[q].slot2 != kNone ? (uint8_t)wp[q].slot2 : kNoSlot;
       s_fl[e] = fl;
       if (fl != kResSlow) s_sc[e] = sc;
     }
@@ -2055,13 +2098,12 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
     if (e >= m) continue;
     const uint64_t k = s_key[e];
     const uint32_t lbk = (uint32_t)(bucket_of(t, k) % kPartBuckets);
-    const uint32_t lo = s_off[lbk], hi = s_off[lbk + 1];
-    const uint32_t r = s_rank[e];
+    const uint32_t lo = s_off[lbk];
+    const uint32_t r = e - lo;
     const uint32_t res = s_fl[e] & kResMask;
     bool bad = res == kResSlow;
     uint32_t nnew = 0;
-    for (uint32_t x = lo; x < hi; x++) {
-      if (s_rank[x] >= r) continue;
+    for (uint32_t x = lo; x < e; x++) {
       if (s_key[x] == k) bad = true;
       if ((s_fl[x] & kResMask) == kResNew) {
         nnew++;
@@ -2073,17 +2115,39 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
   }
   lds_barrier();
 
-  /* S. The rest of a bucket whose parallel pass stopped, by its owner lane. */
+  /* S. The rest of a bucket whose parallel pass stopped, by one lane.  Such
+        buckets are listed so that consecutive lanes take them: the serial
+        work (long and divergent) then occupies as few waves as possible,
+        instead of a few lanes of every wave of the SIMD. */
   uint32_t added = 0;
+  uint32_t hand = kNone;  // hand-over of the bucket this lane took: record << 16 | pool entry
+  uint32_t hand_bk = 0;   // that bucket
   {
     const uint32_t bk = tid;
+    const uint32_t lo = s_off[bk], hi = s_off[bk + 1], c = hi - lo;
+    if (s_cnt[bk] < c) {
+      s_serial[atomicAdd(&s_nser, 1u)] = (uint8_t)bk;
+    } else if (lo < hi) {
+      // Every key of the bucket was applied in parallel.
+      uint32_t bsz = s_bsz[bk];
+      for (uint32_t x = lo; x < hi; x++) bsz += (s_fl[x] & kResMask) == kResNew ? 1u : 0u;
+      s_cnt[bk] = c;
+      if (bsz != s_bsz[bk]) {
+        G(t.bsize)[part_b0 + bk] = (int32_t)bsz;
+        added = bsz - s_bsz[bk];
+      }
+    }
+  }
+  lds_barrier();
+  if (tid < s_nser) {
+    const uint32_t bk = s_serial[tid];
     const uint64_t b = part_b0 + bk;
     const uint32_t lo = s_off[bk], hi = s_off[bk + 1], c = hi - lo;
-    uint32_t stop = s_cnt[bk] < c ? s_cnt[bk] : c;
+    uint32_t stop = s_cnt[bk];
     uint32_t bsz = s_bsz[bk];
     uint32_t f0 = 0, f1 = 0, f2 = 0, f3 = 0;  // slots filled by the call so far
-    for (uint32_t x = lo; x < hi; x++) {
-      if (s_rank[x] < stop && (s_fl[x] & kResMask) == kResNew) {
+    for (uint32_t x = lo; x < lo + stop; x++) {
+      if ((s_fl[x] & kResMask) == kResNew) {
         const uint32_t sl = s_slot[x], bit = 1u << (sl & 31), wq = sl >> 5;
         f0 |= wq == 0 ? bit : 0u;
         f1 |= wq == 1 ? bit : 0u;
@@ -2094,22 +2158,59 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
     }
     const uint64_t base = b * (uint64_t)B;
     for (uint32_t r = stop; r < c; r++) {
-      const uint32_t e = entry_of_rank(s_rank, lo, hi, r);
+      const uint32_t e = lo + r;
       const uint64_t k = s_key[e];
       const uint64_t i = s_idx[e];
       const uint64_t in = has_in ? G(a.in_scores)[i] : 0;
       const uint64_t h = murmur3(k);
       const uint32_t start = (uint32_t)(global_idx(t, h) & (B - 1));
       const uint32_t d = key_digest(h);
-      if (may_insert && bsz >= B) {
+      // Most keys here need no new probe.  A key met earlier in the call is
+      // present at that key's slot; a key present before the call still is
+      // (nothing is evicted here); and the call only removes EMPTY slots, so
+      // a key's first EMPTY slot before the call is still its first one
+      // unless an earlier key of the call took it.
+      int dup = 0;
+      int sl = -1;
+      bool known = false;
+      for (uint32_t x = lo; x < e; x++) {
+        if (s_key[x] == k && s_slot[x] != kNoSlot) {
+          sl = s_slot[x];
+          dup = 1;
+          known = true;
+        }
+      }
+      const uint32_t pres = s_fl[e] & kResMask;  // outcome on the table before the call
+      if (!known && pres == kResDup) {
+        sl = s_slot[e];
+        dup = 1;
+        known = true;
+      }
+      if (!known && may_insert && bsz >= B) {
         // A full bucket: the eviction path (which also finds a present key)
         // takes the rest of it, without a scan of the whole bucket here.
         stop = r;
         break;
       }
-      int dup = 0;
-      const int sl = probe_serial(t, base, f0, f1, f2, f3, s_key, s_slot, s_fl, s_rank, lo, hi, r,
-                                  start, d, k, !may_insert || bsz < B, &dup);
+      if (!known && pres == kResNew) {
+        // If an earlier key took the first EMPTY slot, the probe goes on to
+        // the second (recorded when no digest match lies between them).
+        const uint32_t ts = s_slot[e], ts2 = s_slot2[e];
+        bool taken = false, taken2 = false;
+        for (uint32_t x = lo; x < e; x++) {
+          if ((s_fl[x] & kResMask) == kResNew) {
+            taken |= s_slot[x] == ts;
+            taken2 |= s_slot[x] == ts2;
+          }
+        }
+        if (!taken || (ts2 != kNoSlot && !taken2)) {
+          sl = (int)(taken ? ts2 : ts);
+          known = true;
+        }
+      }
+      if (!known)
+        sl = probe_serial(t, base, f0, f1, f2, f3, s_key, s_slot, s_fl, lo, e, start, d, k,
+                          !may_insert || bsz < B, &dup);
       if (sl < 0 && may_insert) {
         // The eviction path: the rest of the bucket goes to k_apply_deferred.
         stop = r;
@@ -2127,18 +2228,11 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
       bool w;
       // The latest earlier record of the call at this slot, and the latest
       // earlier key whose input row is queued for it.
-      uint32_t xrec = kNone, xin = kNone, rrec = 0, rin = 0;
-      for (uint32_t x = lo; x < hi; x++) {
-        const uint32_t rx = s_rank[x];
-        if (rx >= r || s_slot[x] != slu) continue;
-        if ((s_fl[x] & kMetaMask) && (xrec == kNone || rx > rrec)) {
-          xrec = x;
-          rrec = rx;
-        }
-        if ((s_fl[x] & kTkMask) == kTkIn && (xin == kNone || rx > rin)) {
-          xin = x;
-          rin = rx;
-        }
+      uint32_t xrec = kNone, xin = kNone;
+      for (uint32_t x = lo; x < e; x++) {
+        if (s_slot[x] != slu) continue;
+        if (s_fl[x] & kMetaMask) xrec = x;
+        if ((s_fl[x] & kTkMask) == kTkIn) xin = x;
       }
       if (dup) {
         uint64_t old = 0;
@@ -2177,28 +2271,16 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
       s_slot[e] = (uint8_t)slu;
       s_fl[e] = fl;
     }
-    if (lo < hi) s_cnt[bk] = stop;  // keys of rank < stop are applied here
+    s_cnt[bk] = stop;  // keys of rank < stop are applied here
+    // A bucket handed over takes a record and pool entries, counted here in
+    // LDS; the block reserves them with one pair of atomics below.
     if (stop < c) {
-      // Hand over: a record {bucket, keys, first key left, pool offset} and
-      // the bucket's keys in batch order.
-      const uint32_t rb = atomicAdd(&ps.dctr[0], 1u);
-      const uint32_t po = atomicAdd(&ps.dctr[1], c);
-      gptr<uint32_t> rec = G(ps.drec) + 4 * (uint64_t)rb;
-      rec[0] = (uint32_t)b;
-      rec[1] = c;
-      rec[2] = stop;
-      rec[3] = po;
-      gptr<u64x2> pool = G(reinterpret_cast<u64x2*>(ps.dpool)) + po;
-      for (uint32_t x = lo; x < hi; x++) {
-        u64x2 v;
-        v.x = s_key[x];
-        v.y = s_idx[x];
-        pool[s_rank[x]] = v;
-      }
+      hand = (atomicAdd(&s_nrec, 1u) << 16) | atomicAdd(&s_npool, c);
+      hand_bk = bk;
     }
-    if (lo < hi && bsz != s_bsz[bk]) {
+    if (bsz != s_bsz[bk]) {
       G(t.bsize)[b] = (int32_t)bsz;
-      added = bsz - s_bsz[bk];
+      added += bsz - s_bsz[bk];
     }
   }
   lds_barrier();
@@ -2213,7 +2295,8 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
     const uint64_t k = s_key[e];
     const uint64_t h = murmur3(k);
     const uint64_t gb = global_idx(t, h) >> t.bshift;
-    if (s_rank[e] >= s_cnt[gb % kPartBuckets]) continue;  // left to k_apply_deferred
+    const uint32_t lbk = (uint32_t)(gb % kPartBuckets);
+    if (e - s_off[lbk] >= s_cnt[lbk]) continue;  // left to k_apply_deferred
     const uint64_t s = gb * B + s_slot[e];
     if (f == kMetaKey) {
       slot_store(t, s, k, s_sc[e]);
@@ -2230,6 +2313,31 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
     uint32_t tot = 0;
     for (uint32_t q = 0; q < kBlock / 64; q++) tot += s_wsum[q];
     if (tot) atomicAdd(t.live, (unsigned long long)tot);
+    if (s_nrec) {
+      s_rbase = atomicAdd(&ps.dctr[0], s_nrec);
+      s_pbase = atomicAdd(&ps.dctr[1], s_npool);
+    }
+  }
+  if (s_nrec) {  // uniform in the block
+    lds_barrier();
+    // Hand-over records {bucket, keys, first key left, pool offset} and the
+    // bucket's keys in batch order, for k_apply_deferred.
+    if (hand != kNone) {
+      const uint32_t lo = s_off[hand_bk], hi = s_off[hand_bk + 1];
+      const uint32_t po = s_pbase + (hand & 0xFFFFu);
+      gptr<uint32_t> rec = G(ps.drec) + 4 * (uint64_t)(s_rbase + (hand >> 16));
+      rec[0] = (uint32_t)(part_b0 + hand_bk);
+      rec[1] = hi - lo;
+      rec[2] = s_cnt[hand_bk];
+      rec[3] = po;
+      gptr<u64x2> pool = G(reinterpret_cast<u64x2*>(ps.dpool)) + po;
+      for (uint32_t x = lo; x < hi; x++) {
+        u64x2 v;
+        v.x = s_key[x];
+        v.y = s_idx[x];
+        pool[x - lo] = v;
+      }
+    }
   }
 
   // Row copies of the block's tasks.  Tasks of different keys name different
@@ -2244,7 +2352,8 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
       uint64_t gb = 0;
       if (tk) {
         gb = bucket_of(t, s_key[e]);
-        if (s_rank[e] >= s_cnt[gb % kPartBuckets]) tk = 0;
+        const uint32_t lbk = (uint32_t)(gb % kPartBuckets);
+        if (e - s_off[lbk] >= s_cnt[lbk]) tk = 0;
       }
       if (tk) {
         const uint64_t i = s_idx[e];
@@ -2259,16 +2368,9 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
         } else {
           // The latest earlier key of the bucket whose input row was
           // queued for this slot.
-          const uint32_t lbk = (uint32_t)(gb % kPartBuckets);
-          const uint32_t lo = s_off[lbk], hi = s_off[lbk + 1], r = s_rank[e];
-          uint32_t xs = e, rs = 0;
-          for (uint32_t x = lo; x < hi; x++) {
-            const uint32_t rx = s_rank[x];
-            if (rx < r && s_slot[x] == sl && (s_fl[x] & kTkMask) == kTkIn && (xs == e || rx > rs)) {
-              xs = x;
-              rs = rx;
-            }
-          }
+          uint32_t xs = e;
+          for (uint32_t x = s_off[gb % kPartBuckets]; x < e; x++)
+            if (s_slot[x] == sl && (s_fl[x] & kTkMask) == kTkIn) xs = x;
           src = (uint64_t)(uintptr_t)(a.io_values + (uint64_t)s_idx[xs] * R64);
           dst = (uint64_t)(uintptr_t)(a.io_values + i * R64);
         }
