@@ -41,7 +41,7 @@ class Pair:
 
     def __init__(self, init_capacity, max_capacity=None, dim=16,
                  strategy=O.CUSTOMIZED, vt="f32", max_hbm=None,
-                 max_load_factor=0.5):
+                 max_load_factor=0.5, oracle_threads=1):
         import hkv_amd
         torch = _torch()
         self.torch = torch
@@ -50,7 +50,8 @@ class Pair:
             max_capacity = init_capacity
         self.o = O.Oracle(init_capacity, max_capacity, dim=dim,
                           strategy=strategy, value_type=vt,
-                          max_load_factor=max_load_factor)
+                          max_load_factor=max_load_factor,
+                          threads=oracle_threads)
         self.g = hkv_amd.HashTable("u64", vt, strategy)
         self.g.init(hkv_amd.HashTableOptions(
             init_capacity=init_capacity, max_capacity=max_capacity,
