@@ -1373,6 +1373,71 @@ __device__ __forceinline__ void wave_run_tasks(const ApplyArgs& a, gptr<uint64_t
   wave_copy_pairs<U>(src, dst, row_bytes, s_rows);
 }
 
+// Heavy buckets: buckets that receive more than kLaneMax keys of a partition
+// (duplicate-heavy batches such as Zipf traffic, where one key can occur
+// tens of thousands of times).  When the distinct keys of such a bucket that
+// are absent from the table fit its EMPTY slots, no key of the call can
+// evict or be refused, and the batch-order outcome depends only on
+//   * the order of the new keys' first occurrences (each takes the first
+//     EMPTY slot in circular order from its start slot, as one key would),
+//   * per distinct key, a fold of its occurrences' scores:
+//       Lfu:       sum of the inputs (added to the old score of a present key);
+//       EpochLfu:  (epoch << 32) | min(old low word + sum of input low words,
+//                  0xFFFFFFFF) -- consecutive saturating adds compose into one;
+//                  with the epoch ignored the high word is the last input's;
+//       others:    the desired score of the last occurrence,
+//   * and per occurrence a row copy that the fold fixes: find_or_insert
+//     returns the table row of a present key, or the first occurrence's input
+//     for a new key; the upserts write the last occurrence's input.
+// Such a bucket costs one pass of its distinct keys instead of one serial
+// step per occurrence.  Buckets where that condition fails (or whose keys do
+// not fit the block's key map) keep the serial batch-order walk.
+constexpr uint32_t kMapCap = 1024;   // distinct keys of a partition's heavy buckets
+constexpr uint32_t kMapProbe = 64;   // linear-probe limit of the key map
+constexpr uint32_t kItemCap = 128;   // distinct keys of a bucket without eviction (<= B)
+constexpr uint8_t kHvNone = 0, kHvDone = 1, kHvSerial = 2;
+constexpr uint16_t kMapNew = 0x100;     // key map result: new key ...
+constexpr uint16_t kMapPlaced = 0x200;  // ... placed at the slot in the low byte
+
+__device__ __forceinline__ void group_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+}
+
+__device__ __forceinline__ uint32_t map_home(uint64_t h) {
+  return (uint32_t)(h ^ (h >> 29)) & (kMapCap - 1);
+}
+
+// Final score of a heavy-bucket key from the fold of its occurrences (see
+// above); `sum` is the sum of the inputs (Lfu) or of their low words
+// (EpochLfu), `in_last` the input of the last occurrence.
+template <int OP>
+__device__ __forceinline__ uint64_t heavy_score(const ScoreCtx& c, bool has_in, bool is_new,
+                                                uint64_t old, uint64_t sum, uint64_t in_last) {
+  const uint64_t old_lo = is_new ? 0 : (old & kScoreMask);
+  if (OP == OP_ASSIGN_SCORES) {
+    switch (c.strategy) {
+      case kLru: return c.clock;
+      case kLfu: return old + sum;
+      case kEpochLru: return (c.epoch << 32) | ((c.clock >> 20) & kScoreMask);
+      case kEpochLfu: {
+        const uint64_t lo = old_lo + sum;
+        return (c.epoch << 32) | (lo < kScoreMask ? lo : kScoreMask);
+      }
+      default: return in_last;
+    }
+  }
+  switch (c.strategy) {
+    case kLfu: return is_new ? sum : old + sum;
+    case kEpochLfu: {
+      const uint64_t hi = c.epoch == kIgnoredEpoch ? (in_last >> 32) : c.epoch;
+      const uint64_t lo = old_lo + sum;
+      return (hi << 32) | (lo < kScoreMask ? lo : kScoreMask);
+    }
+    default: return score_desired(c, has_in, in_last);
+  }
+}
+
 template <int OP, int U>
 __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a, PartScratch ps,
                                                          int all) {
@@ -1388,17 +1453,36 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
   __shared__ uint32_t s_perm[kPartBuckets];  // buckets by decreasing key count
   __shared__ uint32_t s_cls[64];             // buckets per key count class
   __shared__ uint32_t s_rows[kBlock / 64][64];
-  __shared__ uint32_t s_dg[kPartBuckets * kDgStride];  // digest rows of the buckets
+  // Digest rows of the buckets (run loop); before the run loop, the key map
+  // and item lists of the heavy-bucket pass.
+  __shared__ __align__(16) uint32_t s_dg[kPartBuckets * kDgStride];
   __shared__ uint32_t s_wsum[kBlock / 64];
   __shared__ uint64_t s_src[kBlock / 64][kQ];
   __shared__ uint64_t s_dst[kBlock / 64][kQ];
-  __shared__ uint32_t s_ndefer, s_c1, s_g;
+  __shared__ uint32_t s_ndefer, s_c1;
+  __shared__ uint32_t s_tot[kPartBuckets];  // entries per bucket over the partition
+  __shared__ uint8_t s_hst[kPartBuckets];   // heavy-bucket state
+  __shared__ uint8_t s_hlist[kPartBuckets];
+  __shared__ uint32_t s_icnt[kBlock / 16];
+  __shared__ uint32_t s_nheavy, s_mfull, s_kept;
+  // Key map {key, fold sum, first / last batch index, result, bucket}.
+  uint64_t* const mkey = reinterpret_cast<uint64_t*>(s_dg);
+  uint64_t* const msum = mkey + kMapCap;
+  uint32_t* const mfirst = reinterpret_cast<uint32_t*>(msum + kMapCap);
+  uint32_t* const mlast = mfirst + kMapCap;
+  uint16_t* const mres = reinterpret_cast<uint16_t*>(mlast + kMapCap);
+  uint8_t* const mbk = reinterpret_cast<uint8_t*>(mres + kMapCap);
+  uint16_t* const items = reinterpret_cast<uint16_t*>(mbk + kMapCap);  // [16][kItemCap]
+  static_assert(kMapCap * (8 + 8 + 4 + 4 + 2 + 1) + (kBlock / 16) * kItemCap * 2 <=
+                    sizeof(uint32_t) * kPartBuckets * kDgStride,
+                "key map fits the digest rows");
   const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const uint32_t NP = ps.np, NG = ps.chunks;
+  const uint32_t NP = ps.np;
   const uint32_t B = t.B;
   const uint32_t R = t.row_bytes;
   const bool has_in = a.in_scores != nullptr;
   gptr<const u64x2> ent = G(reinterpret_cast<const u64x2*>(ps.ent));
+  gptr<u64x2> ent_w = G(reinterpret_cast<u64x2*>(ps.ent));  // in-place compaction
   gptr<uint64_t> trow = G(ps.trow);
   uint32_t added = 0;
   // Every partition (accum_or_assign), else the ones k_apply_fast left.
@@ -1407,26 +1491,322 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
     const uint32_t p = all ? li : ps.plist[li];
     const uint32_t base_e = ps.pinfo[2 * p], m = ps.pinfo[2 * p + 1];
     const uint64_t part_b0 = (uint64_t)p * kPartBuckets;
-    if (tid == 0) s_g = 0;
-    uint32_t c0 = base_e;
-    const uint32_t end_e = base_e + m;
-    while (c0 < end_e) {
-      // This run of entries: the whole partition when it fits, else whole
-      // segments in chunk order.
+    uint32_t m_run = m;  // entries left to the run loop
+    if constexpr (kDeferRows) {
+      /* H0. Entries per bucket over the whole partition (a wave adds the
+         count of its leading lane's bucket with one atomic). */
+      s_tot[tid] = 0;
+      s_hst[tid] = kHvNone;
       if (tid == 0) {
-        uint32_t c1 = end_e;
-        if (m > kPartLds) {
-          uint32_t g = s_g;
-          c1 = c0;
-          while (g < NG) {
-            const uint32_t e = g + 1 < NG ? ps.hist[(uint64_t)(g + 1) * NP + p] : end_e;
-            if (e - c0 > kPartLds) break;
-            c1 = e;
-            g++;
-          }
-          s_g = g;
+        s_nheavy = 0;
+        s_mfull = 0;
+        s_kept = 0;
+      }
+      __syncthreads();
+      for (uint32_t e0 = 0; e0 < m; e0 += kBlock) {
+        const uint32_t e = e0 + tid;
+        const bool v = e < m;
+        const uint32_t bk = v ? (uint32_t)(bucket_of(t, ent[base_e + e].x) % kPartBuckets) : 0u;
+        const uint64_t act = __ballot(v);
+        if (act) {
+          const int ld = __ffsll((unsigned long long)act) - 1;
+          const uint32_t lb = __shfl(bk, ld, 64);
+          const uint64_t same = __ballot(v && bk == lb);
+          if ((int)lane == ld) atomicAdd(&s_tot[lb], (uint32_t)__popcll(same));
+          if (v && bk != lb) atomicAdd(&s_tot[bk], 1u);
         }
-        s_c1 = c1;
+      }
+      __syncthreads();
+      if (s_tot[tid] > kLaneMax) s_hlist[atomicAdd(&s_nheavy, 1u)] = (uint8_t)tid;
+      __syncthreads();
+      const uint32_t nheavy = s_nheavy;
+      if (nheavy) {
+        const bool sum_in = a.sc.strategy == kLfu || a.sc.strategy == kEpochLfu;
+        const bool fold_ok =
+            has_in || !(sum_in || a.sc.strategy == kCustomized);
+        /* H1. Fold the heavy buckets' entries into the key map.  Lanes of a
+           wave that hold the leading lane's key are folded first, with one
+           map update. */
+        for (uint32_t q = tid; q < kMapCap; q += kBlock) {
+          mkey[q] = kEmptyKey;
+          msum[q] = 0;
+          mfirst[q] = kNone;
+          mlast[q] = 0;
+        }
+        __syncthreads();
+        for (uint32_t e0 = 0; e0 < m; e0 += kBlock) {
+          if (*(volatile uint32_t*)&s_mfull) break;  // block-uniform: set before a barrier
+          const uint32_t e = e0 + tid;
+          const bool v = e < m;
+          u64x2 en;
+          en.x = kEmptyKey;
+          en.y = 0;
+          if (v) en = ent[base_e + e];
+          const uint64_t k = en.x;
+          const uint32_t i = (uint32_t)en.y;
+          const uint64_t h = murmur3(k);
+          const uint32_t bk = (uint32_t)((global_idx(t, h) >> t.bshift) % kPartBuckets);
+          const bool hv = v && s_tot[bk] > kLaneMax;
+          uint64_t c = 0;
+          if (hv && sum_in && has_in) {
+            const uint64_t in = G(a.in_scores)[i];
+            c = a.sc.strategy == kLfu ? in : (in & kScoreMask);
+          }
+          uint32_t fmin = i, fmax = i;
+          uint64_t csum = c;
+          bool mine = hv;
+          const uint64_t act = __ballot(hv);
+          if (act) {
+            const int ld = __ffsll((unsigned long long)act) - 1;
+            const uint64_t lk = shfl_u64(k, ld, 64);
+            const bool same = hv && k == lk;
+            const uint64_t sm = __ballot(same);
+            if (__popcll(sm) > 1) {
+              uint32_t r1 = same ? i : kNone, r2 = same ? i : 0u;
+              uint64_t r3 = same ? c : 0;
+#pragma unroll
+              for (int d = 32; d > 0; d >>= 1) {
+                const uint32_t o1 = __shfl_xor(r1, d, 64), o2 = __shfl_xor(r2, d, 64);
+                r1 = o1 < r1 ? o1 : r1;
+                r2 = o2 > r2 ? o2 : r2;
+                r3 += shfl_xor_u64(r3, d, 64);
+              }
+              if (same) {
+                mine = (int)lane == ld;
+                fmin = r1;
+                fmax = r2;
+                csum = r3;
+              }
+            }
+          }
+          if (mine) {
+            uint32_t q = map_home(h);
+            bool ok = false;
+            for (uint32_t pr = 0; pr < kMapProbe; pr++) {
+              const uint64_t cur = atomicCAS(reinterpret_cast<unsigned long long*>(&mkey[q]),
+                                             (unsigned long long)kEmptyKey,
+                                             (unsigned long long)k);
+              if (cur == kEmptyKey || cur == k) {
+                ok = true;
+                break;
+              }
+              q = (q + 1) & (kMapCap - 1);
+            }
+            if (!ok) {
+              s_mfull = 1;
+            } else {
+              atomicMin(&mfirst[q], fmin);
+              atomicMax(&mlast[q], fmax);
+              if (csum) atomicAdd(reinterpret_cast<unsigned long long*>(&msum[q]),
+                                  (unsigned long long)csum);
+              mbk[q] = (uint8_t)bk;
+            }
+          }
+          __syncthreads();
+        }
+        __syncthreads();
+        /* H2. One 16-lane group per heavy bucket: the bucket in registers,
+           its distinct keys looked up, and, when the new ones fit its EMPTY
+           slots, placed in first-occurrence order with folded scores. */
+        const uint32_t gi = tid >> 4, gl = tid & 15;
+        const bool mfull = s_mfull != 0;
+        for (uint32_t hq = gi; hq < nheavy; hq += kBlock / 16) {
+          const uint32_t bk = s_hlist[hq];
+          const uint64_t b = part_b0 + bk;
+          uint16_t* const it = items + gi * kItemCap;
+          bool serial = mfull || !fold_ok;
+          if (gl == 0) s_icnt[gi] = 0;
+          group_sync();
+          if (!serial) {
+            for (uint32_t q = gl; q < kMapCap; q += 16)
+              if (mkey[q] != kEmptyKey && mbk[q] == bk) {
+                const uint32_t r = atomicAdd(&s_icnt[gi], 1u);
+                if (r < kItemCap) it[r] = (uint16_t)q;
+              }
+            group_sync();
+          }
+          const uint32_t ni = s_icnt[gi];
+          if (ni > kItemCap) serial = true;
+          if (serial) {
+            if (gl == 0) s_hst[bk] = kHvSerial;
+            continue;
+          }
+          Bucket16 S;
+          bucket_load(t, S, b, gl);
+          uint32_t ne = 0;
+#pragma unroll
+          for (uint32_t j = 0; j < 8; j++) ne += dg_of(S, j) == kEmptyDigest ? 1u : 0u;
+#pragma unroll
+          for (int d = 8; d > 0; d >>= 1) ne += __shfl_xor(ne, d, 16);
+          // Present keys keep their slot; new keys are marked.
+          uint32_t nnew = 0;
+          for (uint32_t x = 0; x < ni; x++) {
+            const uint32_t q = it[x];
+            const uint64_t k = mkey[q];
+            const uint32_t d = key_digest(murmur3(k));
+            uint32_t best = kNone;
+#pragma unroll
+            for (uint32_t j = 0; j < 8; j++)
+              if (dg_of(S, j) == d && S.key[j] == k) best = gl + 16 * j;
+            best = group_min_u32(best);
+            if (gl == 0) mres[q] = best == kNone ? kMapNew : (uint16_t)best;
+            nnew += best == kNone ? 1u : 0u;
+          }
+          group_sync();
+          if (OP == OP_ASSIGN_SCORES) nnew = 0;  // absent keys are a no-op
+          if (nnew > ne) {
+            if (gl == 0) s_hst[bk] = kHvSerial;
+            continue;
+          }
+          // New keys in order of first occurrence: first EMPTY slot in
+          // circular order from the start slot.
+          for (uint32_t r = 0; r < nnew; r++) {
+            uint32_t bf = kNone, bq = 0;
+            for (uint32_t x = gl; x < ni; x += 16) {
+              const uint32_t q = it[x];
+              if (mres[q] == kMapNew && mfirst[q] < bf) {
+                bf = mfirst[q];
+                bq = q;
+              }
+            }
+#pragma unroll
+            for (int d = 8; d > 0; d >>= 1) {
+              const uint32_t of = __shfl_xor(bf, d, 16), oq = __shfl_xor(bq, d, 16);
+              if (of < bf) {
+                bf = of;
+                bq = oq;
+              }
+            }
+            const uint64_t k = mkey[bq];
+            const uint64_t h = murmur3(k);
+            const uint32_t start = (uint32_t)(global_idx(t, h) & (B - 1));
+            const uint32_t d = key_digest(h);
+            uint32_t rl = kNone;
+#pragma unroll
+            for (uint32_t j = 0; j < 8; j++)
+              if (dg_of(S, j) == kEmptyDigest) {
+                const uint32_t rr = (gl + 16 * j - start) & (B - 1);
+                rl = rr < rl ? rr : rl;
+              }
+            const uint32_t pos = (start + group_min_u32(rl)) & (B - 1);
+            if (gl == (pos & 15u)) {
+              dg_set(S, pos >> 4, d);
+              rec_set(S.key, pos >> 4, k);
+            }
+            if (gl == 0) mres[bq] = (uint16_t)(kMapNew | kMapPlaced | pos);
+            group_sync();
+          }
+          // Folded scores and the slots' records.  The last occurrence's
+          // input score of item x sits in lane x % 16, register x / 16.
+          uint64_t inl[8];
+#pragma unroll
+          for (uint32_t j = 0; j < 8; j++) {
+            const uint32_t x = gl + 16 * j;
+            inl[j] = (has_in && x < ni) ? G(a.in_scores)[mlast[it[x]]] : 0;
+          }
+          int32_t nadd = 0;
+          for (uint32_t x = 0; x < ni; x++) {
+            const uint32_t q = it[x];
+            const uint32_t rs = mres[q];
+            const bool is_new = (rs & kMapNew) != 0;
+            const uint64_t in_last = shfl_u64(rec_get(inl, x >> 4), (int)(x & 15u), 16);
+            if (OP == OP_ASSIGN_SCORES && is_new) continue;
+            const uint32_t pos = rs & 0xFFu;
+            if (gl == (pos & 15u)) {
+              const uint64_t old = rec_get(S.score, pos >> 4);
+              const uint64_t ns = heavy_score<OP>(a.sc, has_in, is_new, old, msum[q], in_last);
+              if (is_new) {
+                const uint64_t k = mkey[q];
+                slot_store(t, S.base + pos, k, ns);
+                G(t.digests)[S.base + pos] = (uint8_t)key_digest(murmur3(k));
+              } else {
+                slot_score(t, S.base + pos) = ns;
+              }
+            }
+            nadd += is_new ? 1 : 0;
+          }
+          if (gl == 0) {
+            if (nadd) {
+              G(t.bsize)[b] = S.bsz + nadd;
+              added += (uint32_t)nadd;
+            }
+            s_hst[bk] = kHvDone;
+          }
+        }
+        __syncthreads();
+        /* H3. Row copies of the folded buckets' occurrences, and the other
+           entries compacted in place (order kept) for the run loop. */
+        for (uint32_t e0 = 0; e0 < m; e0 += kBlock) {
+          const uint32_t e = e0 + tid;
+          const bool v = e < m;
+          u64x2 en;
+          en.x = kEmptyKey;
+          en.y = 0;
+          if (v) en = ent[base_e + e];
+          const uint64_t k = en.x;
+          const uint64_t i = en.y;
+          const uint64_t h = murmur3(k);
+          const uint32_t bk = (uint32_t)((global_idx(t, h) >> t.bshift) % kPartBuckets);
+          const bool done = v && s_hst[bk] == kHvDone;
+          uint64_t src = 0, dst = 0;
+          if (done && OP != OP_ASSIGN_SCORES) {
+            uint32_t q = map_home(h);
+            while (mkey[q] != k) q = (q + 1) & (kMapCap - 1);  // present: inserted in H1
+            const uint32_t rs = mres[q];
+            const uint64_t trow_a = (uint64_t)(uintptr_t)row_ptr(t, part_b0 + bk, rs & 0xFFu);
+            if (OP == OP_FIND_OR_INSERT) {
+              if (!(rs & kMapNew)) {
+                src = trow_a;
+                dst = (uint64_t)(uintptr_t)(a.io_values + i * R);
+              } else if (i == mfirst[q]) {
+                src = (uint64_t)(uintptr_t)(a.in_values + i * R);
+                dst = trow_a;
+              } else {
+                src = (uint64_t)(uintptr_t)(a.io_values + (uint64_t)mfirst[q] * R);
+                dst = (uint64_t)(uintptr_t)(a.io_values + i * R);
+              }
+            } else if (i == mlast[q]) {
+              src = (uint64_t)(uintptr_t)(a.in_values + i * R);
+              dst = trow_a;
+            }
+          }
+          const bool keep = v && !done;
+          const uint64_t km = __ballot(keep);
+          if (lane == 0) s_wsum[wv] = (uint32_t)__popcll(km);
+          __syncthreads();  // every entry of this tile has been read
+          uint32_t pre = s_kept, tot = 0;
+#pragma unroll
+          for (uint32_t q = 0; q < kBlock / 64; q++) {
+            pre += q < wv ? s_wsum[q] : 0u;
+            tot += s_wsum[q];
+          }
+          // The kept entry moves to the number of kept entries before it.
+          if (keep) ent_w[base_e + pre + (uint32_t)__popcll(km & ((1ull << lane) - 1))] = en;
+          wave_copy_pairs<U>(src, dst, R, s_rows[wv]);
+          __syncthreads();
+          if (tid == 0) s_kept += tot;
+        }
+        __syncthreads();
+        m_run = s_kept;
+        __syncthreads();
+      }
+    }
+    uint32_t c0 = base_e;
+    const uint32_t end_e = base_e + m_run;
+    while (c0 < end_e) {
+      // This run of entries: the whole list when it fits, else whole
+      // segments in chunk order.  A segment holds at most kPartChunk =
+      // kPartLds entries of one chunk, so (c0, c0 + kPartLds] holds a chunk
+      // boundary; the run ends at the last one.
+      if (end_e - c0 > kPartLds) {
+        if (tid == 0) s_c1 = c0;
+        __syncthreads();
+        for (uint32_t x = c0 + 1 + tid; x <= c0 + kPartLds; x += kBlock)
+          if (ent[x].y / kPartChunk != ent[x - 1].y / kPartChunk) atomicMax(&s_c1, x);
+        __syncthreads();
+      }
+      if (tid == 0) {
+        if (end_e - c0 <= kPartLds) s_c1 = end_e;
         s_ndefer = 0;
       }
       s_cnt[tid] = 0;

@@ -78,15 +78,15 @@ class Pair:
                                 0, unique_key, ignore)
 
     def find_or_insert(self, keys, values, scores=None, unique_key=True,
-                       clock=12345):
+                       clock=12345, ignore=False):
         n = keys.size
         v = self._vals(values, n)
-        ov = self.o.find_or_insert(keys, v, scores, unique_key, False, clock)
+        ov = self.o.find_or_insert(keys, v, scores, unique_key, ignore, clock)
         gv = to_dev(v)
         self.g.set_lru_clock(clock)
         self.g.find_or_insert(n, to_dev(keys), gv,
                               None if scores is None else to_dev(scores), 0,
-                              unique_key)
+                              unique_key, ignore)
         return ov, to_np(gv, self.np_vt).reshape(n, self.dim)
 
     def insert_and_evict(self, keys, values, scores=None, unique_key=True,
