@@ -1145,6 +1145,7 @@ __global__ __launch_bounds__(kBlock) void k_pcount(TableView t, const uint64_t* 
     ps.dctr[0] = 0;
     ps.dctr[1] = 0;
     ps.dctr[2] = 0;
+    ps.dctr[3] = 0;
   }
   __syncthreads();
 #pragma unroll
@@ -1344,6 +1345,76 @@ __device__ __forceinline__ void wave_copy_pairs_q(uint64_t src, uint64_t dst, ui
   __builtin_amdgcn_wave_barrier();
 }
 
+// Lane `u`'s copy unit, broadcast to the wave (u is wave-uniform).
+__device__ __forceinline__ u32x4 bcast_unit(u32x4 v, uint32_t u) {
+  u32x4 r;
+  r.x = __builtin_amdgcn_readlane(v.x, u);
+  r.y = __builtin_amdgcn_readlane(v.y, u);
+  r.z = __builtin_amdgcn_readlane(v.z, u);
+  r.w = __builtin_amdgcn_readlane(v.w, u);
+  return r;
+}
+__device__ __forceinline__ u32x2 bcast_unit(u32x2 v, uint32_t u) {
+  u32x2 r;
+  r.x = __builtin_amdgcn_readlane(v.x, u);
+  r.y = __builtin_amdgcn_readlane(v.y, u);
+  return r;
+}
+__device__ __forceinline__ uint32_t bcast_unit(uint32_t v, uint32_t u) {
+  return __builtin_amdgcn_readlane(v, u);
+}
+__device__ __forceinline__ uint16_t bcast_unit(uint16_t v, uint32_t u) {
+  return (uint16_t)__builtin_amdgcn_readlane((uint32_t)v, u);
+}
+__device__ __forceinline__ uint8_t bcast_unit(uint8_t v, uint32_t u) {
+  return (uint8_t)__builtin_amdgcn_readlane((uint32_t)v, u);
+}
+
+// Row copies of N tasks per lane (dst == 0: none), for task sets where many
+// tasks read one row (the occurrences of a hot key read its table row, or
+// its first occurrence's input): the source of the wave's first task is
+// loaded once and written by every lane whose task reads it; the other
+// tasks are copied pairwise.
+template <int U, int N>
+__device__ __forceinline__ void wave_copy_tasks(uint64_t (&src)[N], uint64_t (&dst)[N],
+                                                uint32_t row_bytes, uint32_t* s_rows) {
+  using T = typename UnitT<U>::T;
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t units = row_bytes / U;
+  uint64_t lead = 0;
+#pragma unroll
+  for (int r = 0; r < N; r++) {
+    const uint64_t m = __ballot(dst[r] != 0);
+    if (m && !lead) lead = shfl_u64(src[r], __ffsll((unsigned long long)m) - 1, 64);
+  }
+  if (lead && units <= 64) {
+    // lpr lanes per row, one unit each; rpi rows per store instruction, so
+    // every instruction writes whole lines.
+    uint32_t lpr = 64;
+    while (lpr > 1 && lpr / 2 >= units) lpr >>= 1;
+    const uint32_t rpi = 64 / lpr, sub = lane % lpr;
+    const T v = sub < units ? __builtin_nontemporal_load(G<const T>((uintptr_t)lead) + sub) : T{};
+#pragma unroll
+    for (int r = 0; r < N; r++) {
+      const bool use = dst[r] != 0 && src[r] == lead;
+      const uint64_t hm = __ballot(use);
+      if (use) s_rows[__popcll(hm & ((1ull << lane) - 1))] = lane;
+      __builtin_amdgcn_wave_barrier();
+      const uint32_t rows = __popcll(hm);
+      for (uint32_t r0 = 0; r0 < rows; r0 += rpi) {
+        const uint32_t row = r0 + lane / lpr;
+        const uint32_t ol = s_rows[row < rows ? row : 0];
+        const uint64_t d = shfl_u64(dst[r], (int)ol, 64);
+        if (row < rows && sub < units) __builtin_nontemporal_store(v, G<T>((uintptr_t)d) + sub);
+      }
+      __builtin_amdgcn_wave_barrier();
+      if (use) dst[r] = 0;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < N; r++) wave_copy_pairs<U>(src[r], dst[r], row_bytes, s_rows);
+}
+
 // Executes and clears the row tasks of batch indices `i`, one per lane (a
 // lane with valid == false takes part without a task).
 template <int U>
@@ -1373,7 +1444,7 @@ __device__ __forceinline__ void wave_run_tasks(const ApplyArgs& a, gptr<uint64_t
   wave_copy_pairs<U>(src, dst, row_bytes, s_rows);
 }
 
-// Heavy buckets: buckets that receive more than kLaneMax keys of a partition
+// Heavy buckets: buckets that receive more than kHeavyMin keys of a partition
 // (duplicate-heavy batches such as Zipf traffic, where one key can occur
 // tens of thousands of times).  When the distinct keys of such a bucket that
 // are absent from the table fit its EMPTY slots, no key of the call can
@@ -1395,6 +1466,8 @@ __device__ __forceinline__ void wave_run_tasks(const ApplyArgs& a, gptr<uint64_t
 constexpr uint32_t kMapCap = 1024;   // distinct keys of a partition's heavy buckets
 constexpr uint32_t kMapProbe = 64;   // linear-probe limit of the key map
 constexpr uint32_t kItemCap = 128;   // distinct keys of a bucket without eviction (<= B)
+constexpr uint32_t kHvPer = 8;       // entries per thread per tile of the streaming passes
+constexpr uint32_t kHeavyMin = 8;    // a bucket with more entries in its partition is folded
 constexpr uint8_t kHvNone = 0, kHvDone = 1, kHvSerial = 2;
 constexpr uint16_t kMapNew = 0x100;     // key map result: new key ...
 constexpr uint16_t kMapPlaced = 0x200;  // ... placed at the slot in the low byte
@@ -1464,7 +1537,10 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
   __shared__ uint8_t s_hst[kPartBuckets];   // heavy-bucket state
   __shared__ uint8_t s_hlist[kPartBuckets];
   __shared__ uint32_t s_icnt[kBlock / 16];
-  __shared__ uint32_t s_nheavy, s_mfull, s_kept;
+  __shared__ uint32_t s_nheavy, s_mfull, s_kept, s_li;
+  __shared__ uint32_t s_head[kPartBuckets];  // first key map entry of each heavy bucket
+  __shared__ uint64_t s_rbase[kPartBuckets];  // row 0 of each bucket (heavy-bucket copies)
+  __shared__ uint32_t s_hw[kHvPer][kBlock / 64];  // kept entries per sub-tile and wave
   // Key map {key, fold sum, first / last batch index, result, bucket}.
   uint64_t* const mkey = reinterpret_cast<uint64_t*>(s_dg);
   uint64_t* const msum = mkey + kMapCap;
@@ -1473,7 +1549,8 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
   uint16_t* const mres = reinterpret_cast<uint16_t*>(mlast + kMapCap);
   uint8_t* const mbk = reinterpret_cast<uint8_t*>(mres + kMapCap);
   uint16_t* const items = reinterpret_cast<uint16_t*>(mbk + kMapCap);  // [16][kItemCap]
-  static_assert(kMapCap * (8 + 8 + 4 + 4 + 2 + 1) + (kBlock / 16) * kItemCap * 2 <=
+  uint16_t* const mnext = items + (kBlock / 16) * kItemCap;  // next entry of the bucket
+  static_assert(kMapCap * (8 + 8 + 4 + 4 + 2 + 1 + 2) + (kBlock / 16) * kItemCap * 2 <=
                     sizeof(uint32_t) * kPartBuckets * kDgStride,
                 "key map fits the digest rows");
   const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -1487,7 +1564,13 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
   uint32_t added = 0;
   // Every partition (accum_or_assign), else the ones k_apply_fast left.
   const uint32_t nlist = all ? NP : *(volatile uint32_t*)&ps.dctr[2];
-  for (uint32_t li = blockIdx.x; li < nlist; li += gridDim.x) {
+  // Blocks take partitions from a counter, so that a block holding a large
+  // partition is not also given a fixed share of the others.
+  for (;;) {
+    if (tid == 0) s_li = atomicAdd(&ps.dctr[3], 1u);
+    __syncthreads();
+    const uint32_t li = s_li;
+    if (li >= nlist) break;  // block-uniform
     const uint32_t p = all ? li : ps.plist[li];
     const uint32_t base_e = ps.pinfo[2 * p], m = ps.pinfo[2 * p + 1];
     const uint64_t part_b0 = (uint64_t)p * kPartBuckets;
@@ -1497,36 +1580,45 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
          count of its leading lane's bucket with one atomic). */
       s_tot[tid] = 0;
       s_hst[tid] = kHvNone;
+      s_rbase[tid] = part_b0 + tid < t.buckets
+                         ? (uint64_t)(uintptr_t)row_ptr(t, part_b0 + tid, 0) : 0;
       if (tid == 0) {
         s_nheavy = 0;
         s_mfull = 0;
         s_kept = 0;
       }
       __syncthreads();
-      for (uint32_t e0 = 0; e0 < m; e0 += kBlock) {
-        const uint32_t e = e0 + tid;
-        const bool v = e < m;
-        const uint32_t bk = v ? (uint32_t)(bucket_of(t, ent[base_e + e].x) % kPartBuckets) : 0u;
-        const uint64_t act = __ballot(v);
-        if (act) {
-          const int ld = __ffsll((unsigned long long)act) - 1;
-          const uint32_t lb = __shfl(bk, ld, 64);
-          const uint64_t same = __ballot(v && bk == lb);
-          if ((int)lane == ld) atomicAdd(&s_tot[lb], (uint32_t)__popcll(same));
-          if (v && bk != lb) atomicAdd(&s_tot[bk], 1u);
+      for (uint32_t e0 = 0; e0 < m; e0 += kBlock * kHvPer) {
+        uint64_t kq[kHvPer];
+#pragma unroll
+        for (uint32_t r = 0; r < kHvPer; r++) {
+          const uint32_t e = e0 + tid + r * kBlock;
+          kq[r] = e < m ? ent[base_e + e].x : kEmptyKey;
+        }
+#pragma unroll
+        for (uint32_t r = 0; r < kHvPer; r++) {
+          const bool v = e0 + tid + r * kBlock < m;
+          const uint32_t bk = v ? (uint32_t)(bucket_of(t, kq[r]) % kPartBuckets) : 0u;
+          const uint64_t act = __ballot(v);
+          if (act) {
+            const int ld = __ffsll((unsigned long long)act) - 1;
+            const uint32_t lb = __shfl(bk, ld, 64);
+            const uint64_t same = __ballot(v && bk == lb);
+            if ((int)lane == ld) atomicAdd(&s_tot[lb], (uint32_t)__popcll(same));
+            if (v && bk != lb) atomicAdd(&s_tot[bk], 1u);
+          }
         }
       }
       __syncthreads();
-      if (s_tot[tid] > kLaneMax) s_hlist[atomicAdd(&s_nheavy, 1u)] = (uint8_t)tid;
+      s_head[tid] = kNone;
+      if (s_tot[tid] > kHeavyMin) s_hlist[atomicAdd(&s_nheavy, 1u)] = (uint8_t)tid;
       __syncthreads();
       const uint32_t nheavy = s_nheavy;
       if (nheavy) {
         const bool sum_in = a.sc.strategy == kLfu || a.sc.strategy == kEpochLfu;
         const bool fold_ok =
             has_in || !(sum_in || a.sc.strategy == kCustomized);
-        /* H1. Fold the heavy buckets' entries into the key map.  Lanes of a
-           wave that hold the leading lane's key are folded first, with one
-           map update. */
+        /* H1. Fold the heavy buckets' entries into the key map. */
         for (uint32_t q = tid; q < kMapCap; q += kBlock) {
           mkey[q] = kEmptyKey;
           msum[q] = 0;
@@ -1534,72 +1626,111 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
           mlast[q] = 0;
         }
         __syncthreads();
-        for (uint32_t e0 = 0; e0 < m; e0 += kBlock) {
+        for (uint32_t e0 = 0; e0 < m; e0 += kBlock * kHvPer) {
           if (*(volatile uint32_t*)&s_mfull) break;  // block-uniform: set before a barrier
-          const uint32_t e = e0 + tid;
-          const bool v = e < m;
-          u64x2 en;
-          en.x = kEmptyKey;
-          en.y = 0;
-          if (v) en = ent[base_e + e];
-          const uint64_t k = en.x;
-          const uint32_t i = (uint32_t)en.y;
-          const uint64_t h = murmur3(k);
-          const uint32_t bk = (uint32_t)((global_idx(t, h) >> t.bshift) % kPartBuckets);
-          const bool hv = v && s_tot[bk] > kLaneMax;
-          uint64_t c = 0;
-          if (hv && sum_in && has_in) {
-            const uint64_t in = G(a.in_scores)[i];
-            c = a.sc.strategy == kLfu ? in : (in & kScoreMask);
-          }
-          uint32_t fmin = i, fmax = i;
-          uint64_t csum = c;
-          bool mine = hv;
-          const uint64_t act = __ballot(hv);
-          if (act) {
-            const int ld = __ffsll((unsigned long long)act) - 1;
-            const uint64_t lk = shfl_u64(k, ld, 64);
-            const bool same = hv && k == lk;
-            const uint64_t sm = __ballot(same);
-            if (__popcll(sm) > 1) {
-              uint32_t r1 = same ? i : kNone, r2 = same ? i : 0u;
-              uint64_t r3 = same ? c : 0;
+          u64x2 eq[kHvPer];
+          uint64_t hq_[kHvPer], cq[kHvPer];
+          bool hvq[kHvPer];
 #pragma unroll
-              for (int d = 32; d > 0; d >>= 1) {
-                const uint32_t o1 = __shfl_xor(r1, d, 64), o2 = __shfl_xor(r2, d, 64);
-                r1 = o1 < r1 ? o1 : r1;
-                r2 = o2 > r2 ? o2 : r2;
-                r3 += shfl_xor_u64(r3, d, 64);
-              }
-              if (same) {
-                mine = (int)lane == ld;
-                fmin = r1;
-                fmax = r2;
-                csum = r3;
-              }
+          for (uint32_t r = 0; r < kHvPer; r++) {
+            const uint32_t e = e0 + tid + r * kBlock;
+            eq[r].x = kEmptyKey;
+            eq[r].y = 0;
+            if (e < m) eq[r] = ent[base_e + e];
+          }
+#pragma unroll
+          for (uint32_t r = 0; r < kHvPer; r++) {
+            hq_[r] = murmur3(eq[r].x);
+            const uint32_t bk = (uint32_t)((global_idx(t, hq_[r]) >> t.bshift) % kPartBuckets);
+            hvq[r] = e0 + tid + r * kBlock < m && s_tot[bk] > kHeavyMin;
+          }
+#pragma unroll
+          for (uint32_t r = 0; r < kHvPer; r++) {
+            cq[r] = 0;
+            if (hvq[r] && sum_in && has_in) {
+              const uint64_t in = G(a.in_scores)[eq[r].y];
+              cq[r] = a.sc.strategy == kLfu ? in : (in & kScoreMask);
             }
           }
-          if (mine) {
-            uint32_t q = map_home(h);
-            bool ok = false;
-            for (uint32_t pr = 0; pr < kMapProbe; pr++) {
-              const uint64_t cur = atomicCAS(reinterpret_cast<unsigned long long*>(&mkey[q]),
-                                             (unsigned long long)kEmptyKey,
-                                             (unsigned long long)k);
-              if (cur == kEmptyKey || cur == k) {
-                ok = true;
-                break;
-              }
-              q = (q + 1) & (kMapCap - 1);
+          // The wave's leading key (first heavy entry of the tile) is folded
+          // over all of the tile's sub-rounds with one reduction.
+          uint64_t lk = 0;
+          bool have_lead = false;
+#pragma unroll
+          for (uint32_t r = 0; r < kHvPer; r++) {
+            const uint64_t act = __ballot(hvq[r]);
+            if (act && !have_lead) {
+              lk = shfl_u64(eq[r].x, __ffsll((unsigned long long)act) - 1, 64);
+              have_lead = true;
             }
-            if (!ok) {
-              s_mfull = 1;
+          }
+          uint32_t l1 = kNone, l2 = 0;
+          uint64_t l3 = 0;
+          if (have_lead) {
+#pragma unroll
+            for (uint32_t r = 0; r < kHvPer; r++) {
+              if (hvq[r] && eq[r].x == lk) {
+                const uint32_t i = (uint32_t)eq[r].y;
+                l1 = i < l1 ? i : l1;
+                l2 = i > l2 ? i : l2;
+                l3 += cq[r];
+                hvq[r] = false;  // folded into the leader's update
+              }
+            }
+#pragma unroll
+            for (int d = 32; d > 0; d >>= 1) {
+              const uint32_t o1 = __shfl_xor(l1, d, 64), o2 = __shfl_xor(l2, d, 64);
+              l1 = o1 < l1 ? o1 : l1;
+              l2 = o2 > l2 ? o2 : l2;
+              l3 += shfl_xor_u64(l3, d, 64);
+            }
+          }
+          // Map updates: the leader's folded occurrences (lane 0), then every
+          // other heavy entry on its own.
+#pragma unroll
+          for (uint32_t r = 0; r <= kHvPer; r++) {
+            bool mine;
+            uint64_t k, h, csum;
+            uint32_t fmin, fmax;
+            if (r == kHvPer) {
+              mine = have_lead && lane == 0;
+              k = lk;
+              h = murmur3(lk);
+              fmin = l1;
+              fmax = l2;
+              csum = l3;
             } else {
-              atomicMin(&mfirst[q], fmin);
-              atomicMax(&mlast[q], fmax);
-              if (csum) atomicAdd(reinterpret_cast<unsigned long long*>(&msum[q]),
-                                  (unsigned long long)csum);
-              mbk[q] = (uint8_t)bk;
+              mine = hvq[r];
+              k = eq[r].x;
+              h = hq_[r];
+              fmin = fmax = (uint32_t)eq[r].y;
+              csum = cq[r];
+            }
+            if (mine) {
+              const uint32_t bk = (uint32_t)((global_idx(t, h) >> t.bshift) % kPartBuckets);
+              uint32_t q = map_home(h);
+              bool ok = false;
+              for (uint32_t pr = 0; pr < kMapProbe; pr++) {
+                const uint64_t cur = atomicCAS(reinterpret_cast<unsigned long long*>(&mkey[q]),
+                                               (unsigned long long)kEmptyKey,
+                                               (unsigned long long)k);
+                if (cur == kEmptyKey || cur == k) {
+                  // The lane that installs the key links it into its bucket's list.
+                  if (cur == kEmptyKey) mnext[q] = (uint16_t)atomicExch(&s_head[bk], q);
+                  ok = true;
+                  break;
+                }
+                q = (q + 1) & (kMapCap - 1);
+              }
+              if (!ok) {
+                s_mfull = 1;
+              } else {
+                atomicMin(&mfirst[q], fmin);
+                atomicMax(&mlast[q], fmax);
+                if (csum) atomicAdd(reinterpret_cast<unsigned long long*>(&msum[q]),
+                                    (unsigned long long)csum);
+                mbk[q] = (uint8_t)bk;
+              }
             }
           }
           __syncthreads();
@@ -1618,11 +1749,14 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
           if (gl == 0) s_icnt[gi] = 0;
           group_sync();
           if (!serial) {
-            for (uint32_t q = gl; q < kMapCap; q += 16)
-              if (mkey[q] != kEmptyKey && mbk[q] == bk) {
-                const uint32_t r = atomicAdd(&s_icnt[gi], 1u);
-                if (r < kItemCap) it[r] = (uint16_t)q;
+            if (gl == 0) {
+              uint32_t c = 0;
+              for (uint32_t q = s_head[bk]; q != 0xFFFFu && q != kNone; q = mnext[q]) {
+                if (c < kItemCap) it[c] = (uint16_t)q;
+                c++;
               }
+              s_icnt[gi] = c;
+            }
             group_sync();
           }
           const uint32_t ni = s_icnt[gi];
@@ -1734,57 +1868,73 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
           }
         }
         __syncthreads();
-        /* H3. Row copies of the folded buckets' occurrences, and the other
-           entries compacted in place (order kept) for the run loop. */
-        for (uint32_t e0 = 0; e0 < m; e0 += kBlock) {
-          const uint32_t e = e0 + tid;
-          const bool v = e < m;
-          u64x2 en;
-          en.x = kEmptyKey;
-          en.y = 0;
-          if (v) en = ent[base_e + e];
-          const uint64_t k = en.x;
-          const uint64_t i = en.y;
-          const uint64_t h = murmur3(k);
-          const uint32_t bk = (uint32_t)((global_idx(t, h) >> t.bshift) % kPartBuckets);
-          const bool done = v && s_hst[bk] == kHvDone;
-          uint64_t src = 0, dst = 0;
-          if (done && OP != OP_ASSIGN_SCORES) {
-            uint32_t q = map_home(h);
-            while (mkey[q] != k) q = (q + 1) & (kMapCap - 1);  // present: inserted in H1
-            const uint32_t rs = mres[q];
-            const uint64_t trow_a = (uint64_t)(uintptr_t)row_ptr(t, part_b0 + bk, rs & 0xFFu);
-            if (OP == OP_FIND_OR_INSERT) {
-              if (!(rs & kMapNew)) {
-                src = trow_a;
-                dst = (uint64_t)(uintptr_t)(a.io_values + i * R);
-              } else if (i == mfirst[q]) {
+        /* H3. Row copies of the folded buckets' occurrences (find_or_insert:
+           row tasks), and the other entries compacted in place (order kept)
+           for the run loop. */
+        for (uint32_t e0 = 0; e0 < m; e0 += kBlock * kHvPer) {
+          u64x2 eq[kHvPer];
+          uint64_t srcq[kHvPer], dstq[kHvPer];
+          bool keepq[kHvPer];
+#pragma unroll
+          for (uint32_t r = 0; r < kHvPer; r++) {
+            const uint32_t e = e0 + tid + r * kBlock;
+            eq[r].x = kEmptyKey;
+            eq[r].y = 0;
+            if (e < m) eq[r] = ent[base_e + e];
+          }
+#pragma unroll
+          for (uint32_t r = 0; r < kHvPer; r++) {
+            const uint64_t k = eq[r].x;
+            const uint64_t i = eq[r].y;
+            const bool v = e0 + tid + r * kBlock < m;
+            const uint64_t h = murmur3(k);
+            const uint32_t bk = (uint32_t)((global_idx(t, h) >> t.bshift) % kPartBuckets);
+            const bool done = v && s_hst[bk] == kHvDone;
+            uint64_t src = 0, dst = 0;
+            if (done && OP != OP_ASSIGN_SCORES) {
+              uint32_t q = map_home(h);
+              while (mkey[q] != k) q = (q + 1) & (kMapCap - 1);  // present: inserted in H1
+              const uint32_t rs = mres[q];
+              const uint64_t trow_a = s_rbase[bk] + (uint64_t)(rs & 0xFFu) * R;
+              if (OP == OP_FIND_OR_INSERT) {
+                // One copy per occurrence: recorded for k_rowtasks, which
+                // spreads them over the whole GPU.
+                trow[i] = !(rs & kMapNew) ? (kTaskOut | trow_a)
+                          : i == mfirst[q] ? (kTaskIn | trow_a)
+                                           : (kTaskFwd | (uint64_t)mfirst[q]);
+              } else if (i == mlast[q]) {
                 src = (uint64_t)(uintptr_t)(a.in_values + i * R);
                 dst = trow_a;
-              } else {
-                src = (uint64_t)(uintptr_t)(a.io_values + (uint64_t)mfirst[q] * R);
-                dst = (uint64_t)(uintptr_t)(a.io_values + i * R);
               }
-            } else if (i == mlast[q]) {
-              src = (uint64_t)(uintptr_t)(a.in_values + i * R);
-              dst = trow_a;
             }
+            srcq[r] = src;
+            dstq[r] = dst;
+            keepq[r] = v && !done;
           }
-          const bool keep = v && !done;
-          const uint64_t km = __ballot(keep);
-          if (lane == 0) s_wsum[wv] = (uint32_t)__popcll(km);
-          __syncthreads();  // every entry of this tile has been read
-          uint32_t pre = s_kept, tot = 0;
+          uint64_t kmq[kHvPer];
 #pragma unroll
-          for (uint32_t q = 0; q < kBlock / 64; q++) {
-            pre += q < wv ? s_wsum[q] : 0u;
-            tot += s_wsum[q];
+          for (uint32_t r = 0; r < kHvPer; r++) {
+            kmq[r] = __ballot(keepq[r]);
+            if (lane == 0) s_hw[r][wv] = (uint32_t)__popcll(kmq[r]);
           }
-          // The kept entry moves to the number of kept entries before it.
-          if (keep) ent_w[base_e + pre + (uint32_t)__popcll(km & ((1ull << lane) - 1))] = en;
-          wave_copy_pairs<U>(src, dst, R, s_rows[wv]);
+          __syncthreads();  // every entry of this tile has been read
+          // Entries of sub-tile r precede those of sub-tile r + 1; a kept
+          // entry moves to the number of kept entries before it.
+          uint32_t run = s_kept;
+#pragma unroll
+          for (uint32_t r = 0; r < kHvPer; r++) {
+            uint32_t pre = run;
+#pragma unroll
+            for (uint32_t q = 0; q < kBlock / 64; q++) {
+              pre += q < wv ? s_hw[r][q] : 0u;
+              run += s_hw[r][q];
+            }
+            if (keepq[r])
+              ent_w[base_e + pre + (uint32_t)__popcll(kmq[r] & ((1ull << lane) - 1))] = eq[r];
+          }
+          wave_copy_tasks<U, kHvPer>(srcq, dstq, R, s_rows[wv]);
           __syncthreads();
-          if (tid == 0) s_kept += tot;
+          if (tid == 0) s_kept = run;
         }
         __syncthreads();
         m_run = s_kept;
@@ -2084,6 +2234,21 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
 #pragma unroll
   for (int d = 32; d > 0; d >>= 1) added += __shfl_xor(added, d, 64);
   if (lane == 0 && added) atomicAdd(t.live, (unsigned long long)added);
+}
+
+// Executes the row tasks k_apply_part left in the task words (the
+// find_or_insert copies of folded heavy buckets; zero elsewhere), over the
+// whole GPU, and clears them.  The tasks of one call are independent: they
+// read input rows, present keys' table rows or rows no task writes.
+template <int U>
+__global__ __launch_bounds__(kBlock) void k_rowtasks(TableView t, ApplyArgs a, PartScratch ps) {
+  __shared__ uint32_t s_rows[kBlock / 64][64];
+  const uint32_t wv = threadIdx.x >> 6;
+  gptr<uint64_t> trow = G(ps.trow);
+  for (uint64_t i0 = (uint64_t)blockIdx.x * kBlock; i0 < a.n; i0 += (uint64_t)gridDim.x * kBlock) {
+    const uint64_t i = i0 + threadIdx.x;
+    wave_run_tasks<U>(a, trow, i < a.n ? i : 0, i < a.n, t.row_bytes, s_rows[wv]);
+  }
 }
 
 // Single-run apply of a partition whose entries fit one LDS load (kFastLds)
@@ -3123,7 +3288,9 @@ static void apply_part_op(const TableView& t, const ApplyArgs& a, const PartScra
     hipLaunchKernelGGL((k_apply_fast<fast ? OP : 0, UU>), g, b, 0, s, t, a, ps);             \
     hipLaunchKernelGGL((k_apply_deferred<fast ? OP : 0, UU>), gd, b, 0, s, t, a, ps);        \
   }                                                                                          \
-  hipLaunchKernelGGL((k_apply_part<OP, UU>), gp, b, 0, s, t, a, ps, fast ? 0 : 1)
+  hipLaunchKernelGGL((k_apply_part<OP, UU>), gp, b, 0, s, t, a, ps, fast ? 0 : 1);             \
+  if (OP == OP_FIND_OR_INSERT)                                                               \
+    hipLaunchKernelGGL((k_rowtasks<UU>), dim3(grid_for(a.n, kBlock, 2048)), b, 0, s, t, a, ps)
   switch (a.unit) {
     case 16: HKV_PART_U(16); break;
     case 8: HKV_PART_U(8); break;
