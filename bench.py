@@ -58,6 +58,243 @@ def rand_keys(torch, n, gen):
     return torch.where(bad, k - 4, k)
 
 
+def zipf_keys_gpu(torch, n, gen, alpha=1.05, universe=1 << 30):
+    """n Zipf(alpha) keys over [0, universe) on the GPU: Hormann-Derflinger
+    rejection-inversion ranks, mapped through a fixed bijection of the
+    30-bit range so that a key's value says nothing of its rank."""
+    a, N = alpha, float(universe)
+    one = torch.ones((), dtype=torch.float64, device="cuda")
+
+    def H(x):
+        lx = torch.log(x)
+        t = (1.0 - a) * lx
+        return torch.expm1(t) / t * lx
+
+    def H_inv(y):
+        t = y * (1.0 - a)
+        return torch.exp(torch.log1p(t) / t * y)
+
+    hx1 = float(H(one * 1.5)) - 1.0
+    hN = float(H(one * (N + 0.5)))
+    s_ = 2.0 - float(H_inv(H(one * 2.5) - 2.0 ** -a))
+    out = torch.empty(n, dtype=torch.int64, device="cuda")
+    todo = torch.arange(n, device="cuda")
+    while todo.numel():
+        u = hN + torch.rand(todo.numel(), dtype=torch.float64, device="cuda",
+                            generator=gen) * (hx1 - hN)
+        x = H_inv(u)
+        k = torch.clamp(torch.floor(x + 0.5), 1, N)
+        ok = (k - x <= s_) | (u >= H(k + 0.5) - torch.exp(-a * torch.log(k)))
+        out[todo[ok]] = k[ok].to(torch.int64)
+        todo = todo[~ok]
+    m = (1 << 30) - 1
+    x = (out - 1) & m
+    x = (x * 0x2545F491) & m
+    x ^= x >> 15
+    x = (x * 0x1B873593) & m
+    x ^= x >> 13
+    return x
+
+
+def _events(torch, k):
+    return [torch.cuda.Event(enable_timing=True) for _ in range(k)]
+
+
+def bench_c3(torch, hkv_amd, stream, gen, batches=200):
+    """kEpochLfu, capacity 2^27, dim 32: find_or_insert of 2^20 Zipf(1.05)
+    keys per batch (duplicates: unique_key=false, score increment 1),
+    epoch + 1 every 10 batches."""
+    cap, dim, B = 1 << 27, 32, 1 << 20
+    t = hkv_amd.HashTable("u64", "f32", hkv_amd.EvictStrategy.kEpochLfu)
+    t.init(hkv_amd.HashTableOptions(init_capacity=cap, max_capacity=cap,
+                                    max_hbm_for_vectors=cap * dim * 4, dim=dim))
+    keys = [zipf_keys_gpu(torch, B, gen) for _ in range(batches)]
+    vals = torch.rand((B, dim), device="cuda", generator=gen)
+    ones = torch.ones(B, dtype=torch.int64, device="cuda")
+    ev = _events(torch, 2 * batches)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        for b in range(batches):
+            t.set_global_epoch(b // 10)
+            ev[2 * b].record(stream)
+            t.find_or_insert(B, keys[b], vals, ones, stream, False)
+            ev[2 * b + 1].record(stream)
+    torch.cuda.synchronize()
+    ms = [ev[2 * b].elapsed_time(ev[2 * b + 1]) for b in range(batches)]
+    size = t.size()
+    del t, keys
+    tot = sum(ms)
+    return {"op": "find_or_insert (unique_key=false)", "batches": batches,
+            "mkeys_s": round(B * batches / tot / 1e3, 1),
+            "ms_per_batch_mean": round(tot / batches, 4),
+            "ms_last_10": round(sum(ms[-10:]) / 10, 4), "final_size": size}
+
+
+def bench_c4(torch, hkv_amd, stream, gen, reps=3):
+    """kLfu, capacity 2^26, dim 128, prefilled to load factor 1.0 with uint32
+    scores: insert_and_evict, accum_or_assign and assign_scores on 2^20-key
+    batches of 50% new / 50% resident keys."""
+    cap, dim, B = 1 << 26, 128, 1 << 20
+    t = hkv_amd.HashTable("u64", "f32", hkv_amd.EvictStrategy.kLfu)
+    t.init(hkv_amd.HashTableOptions(init_capacity=cap, max_capacity=cap,
+                                    max_hbm_for_vectors=cap * dim * 4, dim=dim))
+    vals = torch.rand((B, dim), device="cuda", generator=gen) * 2 - 1
+
+    def u32s(n):
+        return torch.randint(0, 1 << 32, (n,), dtype=torch.int64, device="cuda",
+                             generator=gen)
+    with torch.cuda.stream(stream):
+        guard = 0
+        filled = []
+        while t.size(stream) < cap and guard < 200:
+            ks = rand_keys(torch, B, gen)
+            t.insert_or_assign(B, ks, vals, u32s(B), stream)
+            filled.append(ks)
+            guard += 1
+        filled = torch.cat(filled)
+        fv = torch.empty((2 * B, dim), dtype=torch.float32, device="cuda")
+        ff = torch.empty(2 * B, dtype=torch.uint8, device="cuda")
+        ek = torch.empty(B, dtype=torch.int64, device="cuda")
+        evv = torch.empty((B, dim), dtype=torch.float32, device="cuda")
+        es = torch.empty(B, dtype=torch.int64, device="cuda")
+        cnt = torch.zeros(1, dtype=torch.int64, device="cuda")
+
+        def mixed():
+            # resident keys drawn uniformly: prefill keys that find reports
+            cand = filled[torch.randint(0, filled.numel(), (2 * B,), device="cuda",
+                                        generator=gen)]
+            t.find(2 * B, cand, fv, ff, None, stream)
+            res = torch.unique(cand[ff.bool()])
+            res = res[torch.randperm(res.numel(), device="cuda", generator=gen)[:B // 2]]
+            q = torch.cat([res, rand_keys(torch, B - res.numel(), gen)])
+            fl = torch.cat([torch.ones(res.numel(), dtype=torch.uint8, device="cuda"),
+                            torch.zeros(B - res.numel(), dtype=torch.uint8, device="cuda")])
+            perm = torch.randperm(B, device="cuda", generator=gen)
+            return q[perm], fl[perm]  # accumulate resident keys, assign new ones
+        out = {}
+        for name in ("insert_and_evict", "accum_or_assign", "assign_scores"):
+            qs = [mixed() for _ in range(reps)]
+            sc = [u32s(B) for _ in range(reps)]
+            deltas = (torch.rand((B, dim), device="cuda", generator=gen) * 0.02 - 0.01)
+            torch.cuda.synchronize()
+            e = _events(torch, 2 * reps)
+            n_ev = 0
+            for r in range(reps):
+                q, fl = qs[r]
+                e[2 * r].record(stream)
+                if name == "insert_and_evict":
+                    cnt.zero_()
+                    t.insert_and_evict(B, q, vals, sc[r], ek, evv, es, cnt, stream)
+                elif name == "accum_or_assign":
+                    t.accum_or_assign(B, q, deltas, fl, sc[r], stream)
+                else:
+                    t.assign_scores(B, q, sc[r], stream)
+                e[2 * r + 1].record(stream)
+            torch.cuda.synchronize()
+            if name == "insert_and_evict":
+                n_ev = int(cnt.item())
+            ms = sum(e[2 * r].elapsed_time(e[2 * r + 1]) for r in range(reps)) / reps
+            out[name] = {"mkeys_s": round(B / ms / 1e3, 1), "ms": round(ms, 4)}
+            if name == "insert_and_evict":
+                out[name]["evicted_last_batch"] = n_ev
+                # half the keys evict: model bytes (evicting upsert + victim
+                # row out + record) for them, present-key upsert for the rest
+                V = 4 * dim
+                b_ev = 8 + 2 * V + 8 * S + 2048 + 8 + V + 16
+                b_hit = 8 + 2 * V + 6 * S + 8
+                gbs = (b_ev + b_hit) / 2 * B / (ms * 1e-3) / 1e9
+                out[name]["algo_gbs"] = round(gbs, 1)
+                out[name]["frac_hbm"] = round(gbs / HBM_PEAK_GBS, 4)
+    del t, filled, fv
+    return out
+
+
+def bench_c5(torch, hkv_amd, stream, gen):
+    """kCustomized, init 2^27 growing to 2^28, dim 64, max_hbm_for_vectors
+    16 GiB (after growth 3/4 of the rows are pinned host memory): fill with
+    2^20-key insert_or_assign batches until auto-growth, time the growing
+    call, mixed find / insert_or_assign batches, then export_batch over the
+    whole table in 2^22-slot chunks."""
+    init, mx, dim, B = 1 << 27, 1 << 28, 64, 1 << 20
+    t = hkv_amd.HashTable("u64", "f32", hkv_amd.EvictStrategy.kCustomized)
+    t.init(hkv_amd.HashTableOptions(init_capacity=init, max_capacity=mx,
+                                    max_hbm_for_vectors=16 << 30, dim=dim))
+    vals = torch.rand((B, dim), device="cuda", generator=gen) * 2 - 1
+    out_v = torch.empty((B, dim), dtype=torch.float32, device="cuda")
+    fnd = torch.empty(B, dtype=torch.uint8, device="cuda")
+    res = {}
+    with torch.cuda.stream(stream):
+        inserted = []
+        grow_ms = None
+        for b in range(80):
+            ks = rand_keys(torch, B, gen)
+            sc = torch.randint(0, 1 << 62, (B,), dtype=torch.int64, device="cuda",
+                               generator=gen)
+            cap0 = t.capacity()
+            torch.cuda.synchronize()
+            a = time.perf_counter()
+            t.insert_or_assign(B, ks, vals, sc, stream)
+            torch.cuda.synchronize()
+            dt = (time.perf_counter() - a) * 1e3
+            if t.capacity() != cap0:
+                grow_ms = round(dt, 2)
+            inserted.append(ks)
+            if t.capacity() == mx and b >= 70:
+                break
+        res["growth_call_ms"] = grow_ms
+        res["capacity"] = t.capacity()
+        allk = torch.cat(inserted)
+        e = _events(torch, 8)
+        for r in range(4):
+            q = allk[torch.randint(0, allk.numel(), (B,), device="cuda", generator=gen)]
+            ks = rand_keys(torch, B, gen)
+            sc = torch.randint(0, 1 << 62, (B,), dtype=torch.int64, device="cuda",
+                               generator=gen)
+            torch.cuda.synchronize()
+            e[0].record(stream)
+            t.find(B, q, out_v, fnd, None, stream)
+            e[1].record(stream)
+            t.insert_or_assign(B, ks, vals, sc, stream)
+            e[2].record(stream)
+            torch.cuda.synchronize()
+            if r == 3:
+                res["find_ms"] = round(e[0].elapsed_time(e[1]), 4)
+                res["insert_or_assign_ms"] = round(e[1].elapsed_time(e[2]), 4)
+        res["find_mkeys_s"] = round(B / res["find_ms"] / 1e3, 1)
+        res["insert_or_assign_mkeys_s"] = round(B / res["insert_or_assign_ms"] / 1e3, 1)
+        C = 1 << 22
+        ek = torch.empty(C, dtype=torch.int64, device="cuda")
+        ev = torch.empty((C, dim), dtype=torch.float32, device="cuda")
+        es = torch.empty(C, dtype=torch.int64, device="cuda")
+        cnt = torch.zeros(1, dtype=torch.int64, device="cuda")
+        total = 0
+        torch.cuda.synchronize()
+        a = time.perf_counter()
+        for off in range(0, t.capacity(), C):
+            t.export_batch(C, off, ek, ev, es, cnt, stream)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - a
+        total = t.size(stream)
+        res["export_s"] = round(dt, 4)
+        res["export_gbs"] = round(total * (8 + 4 * dim + 8) / dt / 1e9, 1)
+        res["size"] = total
+        # host link ceiling for the host-resident rows
+        h = torch.empty(1 << 28, dtype=torch.float32, pin_memory=True)
+        d = torch.empty(1 << 28, dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        a = time.perf_counter()
+        d.copy_(h, non_blocking=True)
+        torch.cuda.synchronize()
+        res["h2d_gbs"] = round((1 << 30) / (time.perf_counter() - a) / 1e9, 1)
+        a = time.perf_counter()
+        h.copy_(d, non_blocking=True)
+        torch.cuda.synchronize()
+        res["d2h_gbs"] = round((1 << 30) / (time.perf_counter() - a) / 1e9, 1)
+        del h, d
+    del t
+    return res
+
+
 def cpu_baseline(seconds_hint=20.0):
     """The oracle on the host cores: kLru, capacity 2^26, dim 64, filled to
     load factor ~0.5, then insert_or_assign of new keys and find of resident
@@ -111,6 +348,10 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the load factor 0.75/1.0 and miss points")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the other benchmark configurations (Zipf "
+                         "find_or_insert, full-table Lfu eviction and "
+                         "accumulation, hybrid HBM/host table)")
     ap.add_argument("--calibrate", action="store_true",
                     help="first run a plain 1 GiB device-to-device copy (the "
                          "reference kernel for scaling HBM byte counters)")
@@ -253,6 +494,18 @@ def main():
                                               None, stream))
             breakdown["find_hit_lf1.0"] = {"mkeys_s": round(BATCH / hf / 1e3, 1),
                                            "ms": round(hf, 4)}
+
+    if not args.no_configs:
+        import gc
+        for name, fn in (("zipf_epoch_lfu_cap2^27_dim32", bench_c3),
+                         ("lfu_full_table_cap2^26_dim128", bench_c4),
+                         ("hybrid_customized_cap2^27to2^28_dim64", bench_c5)):
+            try:
+                breakdown[name] = fn(torch, hkv_amd, stream, gen)
+            except Exception as exc:  # reported, never fatal for the main line
+                breakdown[name] = {"error": repr(exc)}
+            gc.collect()
+            torch.cuda.empty_cache()
 
     # The dominant operation of the step sets the roofline line.
     if ins_ms >= find_ms:

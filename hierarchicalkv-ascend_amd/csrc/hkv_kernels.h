@@ -30,6 +30,8 @@ struct ApplyArgs {
   uint8_t* ev_values;
   uint64_t* ev_scores;
   uint64_t* ev_counter;
+  uint32_t* ev_bits;          // insert_and_evict: records at their batch index, flagged here
+                              // (null: records appended at an atomic counter)
   uint64_t n;
   ScoreCtx sc;
   int rule;
@@ -59,7 +61,11 @@ struct PartScratch {
   uint32_t* plist;      // [partitions] partitions the single-run kernel left
   uint32_t* drec;       // [n][4] buckets handed to the 16-lane kernel
   uint64_t* dpool;      // [n][2] their keys, {key, batch index}
-  uint32_t* dctr;       // [3] records, pool entries, listed partitions (zeroed by the count kernel)
+  uint32_t* dctr;       // [4] records, pool entries, listed partitions, partitions taken
+                        // (zeroed by the count kernel)
+  uint32_t* ev_bits;    // [n / 32 + 1] insert_and_evict record flags, zero between calls
+  uint32_t* ev_wpre;    // [n / 32 + 1] set bits before each word, within its block of 256 words
+  uint32_t* ev_blk;     // [n / 8192 + 3] block offsets, then the record count and records below it
   uint32_t np;          // partitions
   uint32_t chunks;      // batch chunks
   uint32_t cap;         // fixed region size per partition (entries)

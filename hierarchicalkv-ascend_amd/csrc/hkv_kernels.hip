@@ -466,6 +466,20 @@ __device__ __forceinline__ void accum_row(gptr<uint8_t> dst, gptr<const uint8_t>
   }
 }
 
+// Output position of the eviction record of batch key `i` (all 16 lanes of
+// the group call this): the key's own batch index, flagged for the
+// compaction kernels, or (without a flag bitmap) the next value of the
+// record counter.
+__device__ __forceinline__ uint64_t ev_slot(const ApplyArgs& a, uint64_t i, uint32_t l) {
+  if (a.ev_bits) {
+    if (l == 0) atomicOr(&a.ev_bits[i >> 5], 1u << (i & 31));
+    return i;
+  }
+  uint64_t j = 0;
+  if (l == 0) j = atomicAdd(reinterpret_cast<unsigned long long*>(a.ev_counter), 1ull);
+  return shfl_u64(j, 0, 16);
+}
+
 // Applies batch key `i` to the bucket held by the group (all 16 lanes call
 // this with the same i).  Restates, for one key, the reference kernels
 // insert_or_assign_kernel.h:76-303 (unique keys) and find_and_lock
@@ -581,9 +595,7 @@ __device__ __forceinline__ void apply_key(const TableView& t, Bucket16& S, const
   }
   if (res == R_REFUSED) {
     if (OP == OP_INSERT_AND_EVICT) {
-      uint64_t j = 0;
-      if (l == 0) j = atomicAdd(reinterpret_cast<unsigned long long*>(a.ev_counter), 1ull);
-      j = shfl_u64(j, 0, 16);
+      const uint64_t j = ev_slot(a, i, l);
       if (l == 0) {
         G(a.ev_keys)[j] = k;
         if (a.ev_scores) G(a.ev_scores)[j] = des;
@@ -594,9 +606,7 @@ __device__ __forceinline__ void apply_key(const TableView& t, Bucket16& S, const
   }
   gptr<uint8_t> trow = row_ptr(t, S.b, pos);
   if (OP == OP_INSERT_AND_EVICT && res == R_EVICT) {
-    uint64_t j = 0;
-    if (l == 0) j = atomicAdd(reinterpret_cast<unsigned long long*>(a.ev_counter), 1ull);
-    j = shfl_u64(j, 0, 16);
+    const uint64_t j = ev_slot(a, i, l);
     if (l == 0) {
       G(a.ev_keys)[j] = victim_key;
       if (a.ev_scores) G(a.ev_scores)[j] = victim_score;
@@ -2236,6 +2246,131 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
   if (lane == 0 && added) atomicAdd(t.live, (unsigned long long)added);
 }
 
+/* ------------------------------------------------------------------------ */
+/* insert_and_evict record compaction                                        */
+/* ------------------------------------------------------------------------ */
+
+// The partition pipeline writes the eviction record of batch key i at
+// position i of the caller's output arrays (which hold n records) and flags
+// bit i, instead of appending at an atomically incremented counter (one
+// atomic per record on one address serialises the whole eviction path).
+// These kernels then produce the reference's compact output: with c records
+// in all, the k-th record at a position >= c moves into the k-th hole below
+// c (sources and destinations are disjoint, so every move runs in
+// parallel), the counter gets c, and the flags are cleared.
+constexpr uint32_t kEvBlkWords = 256;  // bitmap words per block of the count kernel
+
+__device__ __forceinline__ uint32_t block_excl_scan256(uint32_t v, uint32_t* s_w,
+                                                        uint32_t* total) {
+  const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  uint32_t x = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t y = __shfl_up(x, d, 64);
+    if (lane >= (uint32_t)d) x += y;
+  }
+  if (lane == 63) s_w[wv] = x;
+  __syncthreads();
+  uint32_t pre = 0, tot = 0;
+#pragma unroll
+  for (uint32_t q = 0; q < kBlock / 64; q++) {
+    pre += q < wv ? s_w[q] : 0u;
+    tot += s_w[q];
+  }
+  __syncthreads();
+  *total = tot;
+  return pre + x - v;
+}
+
+// Set bits before each word within its block, and each block's total.
+__global__ __launch_bounds__(kBlock) void k_evc_count(const uint32_t* __restrict__ bits,
+                                                      uint32_t nw, uint32_t* __restrict__ wpre,
+                                                      uint32_t* __restrict__ blk) {
+  __shared__ uint32_t s_w[kBlock / 64];
+  const uint32_t w = blockIdx.x * kEvBlkWords + threadIdx.x;
+  const uint32_t c = w < nw ? (uint32_t)__popc(bits[w]) : 0u;
+  uint32_t tot;
+  const uint32_t ex = block_excl_scan256(c, s_w, &tot);
+  if (w < nw) wpre[w] = ex;
+  if (threadIdx.x == 0) blk[blockIdx.x] = tot;
+}
+
+__device__ __forceinline__ uint32_t ev_bits_before_word(const uint32_t* blk, const uint32_t* wpre,
+                                                        uint32_t w) {
+  return blk[w / kEvBlkWords] + wpre[w];
+}
+
+// One block: exclusive scan of the block totals; then blk[nb] = c, the
+// record count, and blk[nb + 1] = the records at positions below c; the
+// caller's counter gets c.
+__global__ __launch_bounds__(kBlock) void k_evc_scan(uint32_t* __restrict__ blk, uint32_t nb,
+                                                     const uint32_t* __restrict__ bits,
+                                                     const uint32_t* __restrict__ wpre,
+                                                     uint32_t nw, uint64_t* counter) {
+  __shared__ uint32_t s_w[kBlock / 64];
+  uint32_t carry = 0;
+  for (uint32_t b0 = 0; b0 < nb; b0 += kBlock) {
+    const uint32_t b = b0 + threadIdx.x;
+    const uint32_t v = b < nb ? blk[b] : 0u;
+    uint32_t tot;
+    const uint32_t ex = block_excl_scan256(v, s_w, &tot);
+    if (b < nb) blk[b] = carry + ex;
+    carry += tot;
+  }
+  __syncthreads();  // the scanned offsets are read below
+  if (threadIdx.x == 0) {
+    const uint32_t c = carry;
+    const uint32_t w = c / 32;
+    const uint32_t below =
+        w < nw ? ev_bits_before_word(blk, wpre, w) + (uint32_t)__popc(bits[w] & ((1u << (c & 31)) - 1u))
+               : c;
+    blk[nb] = c;
+    blk[nb + 1] = below;
+    atomicAdd(reinterpret_cast<unsigned long long*>(counter), (unsigned long long)c);
+  }
+}
+
+// Moves every record at a position >= c into a hole below c.
+template <int U>
+__global__ __launch_bounds__(kBlock) void k_evc_move(const uint32_t* __restrict__ bits,
+                                                     uint32_t nw,
+                                                     const uint32_t* __restrict__ wpre,
+                                                     const uint32_t* __restrict__ blk, uint32_t nb,
+                                                     uint64_t n, uint64_t* keys, uint8_t* vals,
+                                                     uint64_t* scores, uint32_t row_bytes) {
+  __shared__ uint32_t s_rows[kBlock / 64][64];
+  const uint32_t wv = threadIdx.x >> 6;
+  const uint32_t c = blk[nb], below = blk[nb + 1];
+  for (uint64_t i0 = (uint64_t)blockIdx.x * kBlock; i0 < n; i0 += (uint64_t)gridDim.x * kBlock) {
+    const uint64_t i = i0 + threadIdx.x;
+    uint64_t src = 0, dst = 0;
+    if (i < n && i >= c) {
+      const uint32_t w = (uint32_t)(i >> 5), word = bits[w];
+      if ((word >> (i & 31)) & 1u) {
+        // rank among the records at positions >= c = rank of its hole
+        const uint32_t r = ev_bits_before_word(blk, wpre, w) +
+                           (uint32_t)__popc(word & ((1u << (i & 31)) - 1u)) - below;
+        // last word x <= (c - 1) / 32 with (holes before x) <= r
+        uint32_t lo = 0, hi = (c - 1) / 32;
+        while (lo < hi) {
+          const uint32_t mid = (lo + hi + 1) / 2;
+          if (32 * mid - ev_bits_before_word(blk, wpre, mid) <= r) lo = mid;
+          else hi = mid - 1;
+        }
+        uint32_t inv = ~bits[lo];
+        for (uint32_t k = r - (32 * lo - ev_bits_before_word(blk, wpre, lo)); k > 0; k--)
+          inv &= inv - 1;
+        const uint64_t h = 32ull * lo + (uint32_t)(__ffs(inv) - 1);
+        keys[h] = keys[i];
+        if (scores) scores[h] = scores[i];
+        src = (uint64_t)(uintptr_t)(vals + i * row_bytes);
+        dst = (uint64_t)(uintptr_t)(vals + h * row_bytes);
+      }
+    }
+    wave_copy_pairs<U>(src, dst, row_bytes, s_rows[wv]);
+  }
+}
+
 // Executes the row tasks k_apply_part left in the task words (the
 // find_or_insert copies of folded heavy buckets; zero elsewhere), over the
 // whole GPU, and clears them.  The tasks of one call are independent: they
@@ -3283,6 +3418,8 @@ static void apply_part_op(const TableView& t, const ApplyArgs& a, const PartScra
   // walk device-side lists that are usually empty: small grids.
   const dim3 gd(grid_for(a.n * 16, kBlock, 2048));
   const dim3 gp(fast ? (ps.np < 256 ? ps.np : 256) : ps.np);
+  const uint32_t nw = (uint32_t)((a.n + 31) / 32);
+  const uint32_t nbw = (nw + kEvBlkWords - 1) / kEvBlkWords;
 #define HKV_PART_U(UU)                                                                       \
   if constexpr (fast) {                                                                      \
     hipLaunchKernelGGL((k_apply_fast<fast ? OP : 0, UU>), g, b, 0, s, t, a, ps);             \
@@ -3290,7 +3427,16 @@ static void apply_part_op(const TableView& t, const ApplyArgs& a, const PartScra
   }                                                                                          \
   hipLaunchKernelGGL((k_apply_part<OP, UU>), gp, b, 0, s, t, a, ps, fast ? 0 : 1);             \
   if (OP == OP_FIND_OR_INSERT)                                                               \
-    hipLaunchKernelGGL((k_rowtasks<UU>), dim3(grid_for(a.n, kBlock, 2048)), b, 0, s, t, a, ps)
+    hipLaunchKernelGGL((k_rowtasks<UU>), dim3(grid_for(a.n, kBlock, 2048)), b, 0, s, t, a, ps); \
+  if (OP == OP_INSERT_AND_EVICT && a.ev_bits) {                                              \
+    hipLaunchKernelGGL(k_evc_count, dim3(nbw), b, 0, s, ps.ev_bits, nw, ps.ev_wpre, ps.ev_blk); \
+    hipLaunchKernelGGL(k_evc_scan, dim3(1), b, 0, s, ps.ev_blk, nbw, ps.ev_bits, ps.ev_wpre,   \
+                       nw, a.ev_counter);                                                    \
+    hipLaunchKernelGGL((k_evc_move<UU>), dim3(grid_for(a.n, kBlock, 2048)), b, 0, s,         \
+                       ps.ev_bits, nw, ps.ev_wpre, ps.ev_blk, nbw, a.n, a.ev_keys,          \
+                       a.ev_values, a.ev_scores, t.row_bytes);                               \
+    launch_fill_u32(ps.ev_bits, 0, nw, s);                                                   \
+  }
   switch (a.unit) {
     case 16: HKV_PART_U(16); break;
     case 8: HKV_PART_U(8); break;

@@ -126,6 +126,10 @@ struct hkv_table {
   uint64_t* p_dpool = nullptr;
   uint64_t p_defer_cap = 0;
   uint32_t* p_dctr = nullptr;
+  uint32_t* p_evbits = nullptr;  // insert_and_evict record flags (zero between calls)
+  uint32_t* p_evwpre = nullptr;
+  uint32_t* p_evblk = nullptr;
+  uint64_t p_evw_cap = 0;
   // export scratch
   uint32_t* blk = nullptr;
   uint64_t blk_cap = 0;
@@ -221,6 +225,9 @@ struct hkv_table {
     (void)hipFree(p_drec);
     (void)hipFree(p_dpool);
     (void)hipFree(p_dctr);
+    (void)hipFree(p_evbits);
+    (void)hipFree(p_evwpre);
+    (void)hipFree(p_evblk);
     (void)hipFree(blk);
     (void)hipFree(d_sum);
     if (h_sum) (void)hipHostFree(h_sum);
@@ -296,8 +303,20 @@ struct hkv_table {
       p_defer_cap = n;
     }
     if (!p_dctr) hip_check(hipMalloc(&p_dctr, 4 * sizeof(uint32_t)), "hipMalloc(part counters)");
-    *ps = PartScratch{p_hist, p_ent,  p_info,  p_spill,      p_trow,       p_list,
-                      p_drec, p_dpool, p_dctr, (uint32_t)np, (uint32_t)ng, (uint32_t)cap};
+    const uint64_t nw = n / 32 + 1;
+    if (nw > p_evw_cap) {
+      if (p_evbits) hip_check(hipFree(p_evbits), "hipFree");
+      if (p_evwpre) hip_check(hipFree(p_evwpre), "hipFree");
+      if (p_evblk) hip_check(hipFree(p_evblk), "hipFree");
+      hip_check(hipMalloc(&p_evbits, nw * sizeof(uint32_t)), "hipMalloc(evict flags)");
+      hip_check(hipMalloc(&p_evwpre, nw * sizeof(uint32_t)), "hipMalloc(evict prefix)");
+      hip_check(hipMalloc(&p_evblk, (nw / 256 + 4) * sizeof(uint32_t)), "hipMalloc(evict blocks)");
+      launch_fill_u32(p_evbits, 0, nw, s);
+      p_evw_cap = nw;
+    }
+    *ps = PartScratch{p_hist,  p_ent,   p_info,       p_spill,      p_trow,
+                      p_list,  p_drec,  p_dpool,      p_dctr,       p_evbits,
+                      p_evwpre, p_evblk, (uint32_t)np, (uint32_t)ng, (uint32_t)cap};
     return true;
   }
 
@@ -464,6 +483,7 @@ int insert_like(hkv_table* t, int op, uint64_t n, const void* keys, const void* 
   a.value_type = t->value_type;
   PartScratch ps{};
   if (t->part_scratch(n, &ps, s)) {
+    if (op == OP_INSERT_AND_EVICT) a.ev_bits = ps.ev_bits;
     launch_apply_part(t->view(), op, a, ps, s);
   } else {
     const uint32_t P = t->pick_P(n);

@@ -180,3 +180,23 @@ class Pair:
         np.testing.assert_array_equal(gv.view(np.uint8), ov.view(np.uint8))
         np.testing.assert_array_equal(gs[of], os_[of])
         return of
+
+
+def records_equal(o, g):
+    """Evicted-record multisets equal: (key, score, row bytes) as one sort
+    key, since record order is unspecified and a key can leave two records
+    with the same score in one call (evicted, then refused)."""
+    ok, ov, os_ = o
+    gk, gv, gs = g
+    assert gk.size == ok.size
+    if ok.size == 0:
+        return
+
+    def table(k, v, s):
+        return np.concatenate([k.reshape(-1, 1).view(np.uint8), s.reshape(-1, 1).view(np.uint8),
+                               np.ascontiguousarray(v).reshape(k.size, -1).view(np.uint8)],
+                              axis=1)
+    a, b = table(ok, ov, os_), table(gk, gv, gs)
+    a = a[np.lexsort(a.T[::-1])] if a.size else a
+    b = b[np.lexsort(b.T[::-1])] if b.size else b
+    np.testing.assert_array_equal(b, a)

@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from gpu_pair import Pair
+from gpu_pair import Pair, records_equal
 from helpers import murmur3_np, uniform_keys
 
 pytestmark = pytest.mark.gpu
@@ -107,13 +107,8 @@ def test_single_run_insert_and_evict_and_assign_scores():
         ks = pool[1024 * b:1024 * (b + 1)] if b % 2 == 0 else rng.choice(pool[:1024 * b], 1024,
                                                                           replace=False)
         sc = rng.integers(0, 1 << 20, 1024, dtype=np.uint64)
-        (ok, ov, os_), (gk, gv, gs) = p.insert_and_evict(ks, rand_vals(rng, 1024, 4), sc,
-                                                         clock=b)
-        o1 = np.lexsort((os_, ok))
-        o2 = np.lexsort((gs, gk))
-        np.testing.assert_array_equal(gk[o2], ok[o1])
-        np.testing.assert_array_equal(gs[o2], os_[o1])
-        np.testing.assert_array_equal(gv[o2].view(np.uint8), ov[o1].view(np.uint8))
+        o, g = p.insert_and_evict(ks, rand_vals(rng, 1024, 4), sc, clock=b)
+        records_equal(o, g)
         if b % 8 == 7:
             p.assign_scores(rng.choice(pool[:1024 * (b + 1)], 1024, replace=False),
                             rng.integers(0, 1 << 10, 1024, dtype=np.uint64))

@@ -18,7 +18,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from gpu_pair import Pair
+from gpu_pair import Pair, records_equal
 from helpers import (RESERVED_MASK, murmur3_np, scramble30, uniform_keys,
                      uniform_keys_fast, zipf_ranks)
 
@@ -287,15 +287,6 @@ def test_c3_full_size_zipf_epoch_lfu_properties():
 
 # -- config 4: kLfu, dim 128, full table: insert_and_evict, accum, scores -----
 
-def _records_equal(o, g):
-    ok, ov, os_ = o
-    gk, gv, gs = g
-    assert gk.size == ok.size
-    oo = np.lexsort((os_, ok))
-    go = np.lexsort((gs, gk))
-    np.testing.assert_array_equal(gk[go], ok[oo])
-    np.testing.assert_array_equal(gs[go], os_[oo])
-    np.testing.assert_array_equal(gv[go].view(np.uint8), ov[oo].view(np.uint8))
 
 
 def test_c4_shape_lfu_evict_accum_scores():
@@ -325,7 +316,7 @@ def test_c4_shape_lfu_evict_accum_scores():
         o, g = p.insert_and_evict(q, rand_vals(rng, B, dim),
                                   rng.integers(0, 1 << 32, B, dtype=np.uint64))
         assert g[0].size >= B // 2
-        _records_equal(o, g)
+        records_equal(o, g)
         p.assert_same_state()
         q, flags = mixed()
         flags[:64] ^= 1  # a few mismatched flags: no-ops

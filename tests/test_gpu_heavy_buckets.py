@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from gpu_pair import Pair
+from gpu_pair import Pair, records_equal
 from helpers import keys_in_bucket, uniform_keys
 
 pytestmark = pytest.mark.gpu
@@ -42,15 +42,6 @@ def scores_for(strategy, rng, n, big=False):
     return rng.integers(0, 1000, n, dtype=np.uint64)
 
 
-def _records_equal(o, g):
-    ok, ov, os_ = o
-    gk, gv, gs = g
-    assert gk.size == ok.size
-    oo = np.lexsort((os_, ok))
-    go = np.lexsort((gs, gk))
-    np.testing.assert_array_equal(gk[go], ok[oo])
-    np.testing.assert_array_equal(gs[go], os_[oo])
-    np.testing.assert_array_equal(gv[go].view(np.uint8), ov[oo].view(np.uint8))
 
 
 def _run(p, op, rng, q, strategy, dim, clock, big=False, unique=False):
@@ -63,7 +54,7 @@ def _run(p, op, rng, q, strategy, dim, clock, big=False, unique=False):
         np.testing.assert_array_equal(gv.view(np.uint32), ov.view(np.uint32))
     elif op == "insert_and_evict":
         o, g = p.insert_and_evict(q, v, sc, unique_key=unique, clock=clock)
-        _records_equal(o, g)
+        records_equal(o, g)
     else:
         p.assign_scores(q, sc, clock=clock)
     p.assert_same_state()

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from gpu_pair import Pair, to_dev, to_np
+from gpu_pair import Pair, records_equal, to_dev, to_np
 from helpers import keys_in_bucket, uniform_keys, values_for
 from test_oracle import _strategy_case, _expected_epochlfu
 
@@ -157,15 +157,6 @@ def test_find_or_insert(strategy, unique):
         p.assert_same_state()
 
 
-def _records_equal(o, g):
-    ok, ov, os_ = o
-    gk, gv, gs = g
-    assert gk.size == ok.size
-    oo = np.lexsort((os_, ok))
-    go = np.lexsort((gs, gk))
-    np.testing.assert_array_equal(gk[go], ok[oo])
-    np.testing.assert_array_equal(gs[go], os_[oo])
-    np.testing.assert_array_equal(gv[go].view(np.uint8), ov[oo].view(np.uint8))
 
 
 @pytest.mark.parametrize("strategy,unique", [(O.CUSTOMIZED, True), (O.LFU, True),
@@ -181,7 +172,7 @@ def test_insert_and_evict(strategy, unique):
         sc = None if strategy == O.LRU else rng.integers(0, 100, ks.size, dtype=np.uint64)
         o, g = p.insert_and_evict(ks, rand_vals(rng, ks.size, 16), sc, unique,
                                   clock=500 + b)
-        _records_equal(o, g)
+        records_equal(o, g)
         p.assert_same_state()
 
 
@@ -196,7 +187,7 @@ def test_insert_and_evict_rejects_low_scores():
     lo = keys_in_bucket(rng, 64, cap, 0, lo=100_000_000, hi=200_000_000)
     o, g = p.insert_and_evict(lo, values_for(lo, dim), np.arange(64, dtype=np.uint64))
     assert g[0].size == 64
-    _records_equal(o, g)
+    records_equal(o, g)
     p.assert_same_state()
 
 
