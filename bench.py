@@ -31,11 +31,11 @@ BATCH = 1 << 20
 
 # HBM bytes per key that each operation's kernels move at this workload, from
 # rocprofv3 FETCH_SIZE and WRITE_SIZE passes over
-# `bench.py --no-cpu-baseline --no-extra --steps 4 --warmup 1 --calibrate`,
+# `bench.py --no-cpu-baseline --no-extra --no-configs --steps 4 --warmup 1 --calibrate`,
 # scaled by the factors a plain 1 GiB device copy gives in the same run
 # (fetch x2.0, write x1.0); the per-kernel figures are in
 # profiles/insert_or_assign_find_cap64M_dim64_hbm_bytes.md.
-MEASURED_BYTES_PER_KEY = {"insert_new": 737.6, "find_hit": 661.7}
+MEASURED_BYTES_PER_KEY = {"insert_new": 735.7, "find_hit": 661.7}
 
 
 def algo_bytes(op, dim=DIM):
@@ -295,6 +295,21 @@ def bench_c5(torch, hkv_amd, stream, gen):
     return res
 
 
+def run_configs(torch, hkv_amd, stream, gen):
+    import gc
+    out = {}
+    for name, fn in (("zipf_epoch_lfu_cap2^27_dim32", bench_c3),
+                     ("lfu_full_table_cap2^26_dim128", bench_c4),
+                     ("hybrid_customized_cap2^27to2^28_dim64", bench_c5)):
+        try:
+            out[name] = fn(torch, hkv_amd, stream, gen)
+        except Exception as exc:  # reported, never fatal for the main line
+            out[name] = {"error": repr(exc)}
+        gc.collect()
+        torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(seconds_hint=20.0):
     """The oracle on the host cores: kLru, capacity 2^26, dim 64, filled to
     load factor ~0.5, then insert_or_assign of new keys and find of resident
@@ -352,6 +367,9 @@ def main():
                     help="skip the other benchmark configurations (Zipf "
                          "find_or_insert, full-table Lfu eviction and "
                          "accumulation, hybrid HBM/host table)")
+    ap.add_argument("--configs-only", action="store_true",
+                    help="run only the other benchmark configurations and print "
+                         "their figures as one JSON object")
     ap.add_argument("--calibrate", action="store_true",
                     help="first run a plain 1 GiB device-to-device copy (the "
                          "reference kernel for scaling HBM byte counters)")
@@ -377,6 +395,9 @@ def main():
     stream = torch.cuda.Stream(device=dev)
     gen = torch.Generator(device="cuda")
     gen.manual_seed(1234)
+    if args.configs_only:
+        print(json.dumps(run_configs(torch, hkv_amd, stream, gen)), flush=True)
+        return
     table = hkv_amd.HashTable("u64", "f32", hkv_amd.EvictStrategy.kLru)
     table.init(hkv_amd.HashTableOptions(
         init_capacity=CAP, max_capacity=CAP,
@@ -496,16 +517,7 @@ def main():
                                            "ms": round(hf, 4)}
 
     if not args.no_configs:
-        import gc
-        for name, fn in (("zipf_epoch_lfu_cap2^27_dim32", bench_c3),
-                         ("lfu_full_table_cap2^26_dim128", bench_c4),
-                         ("hybrid_customized_cap2^27to2^28_dim64", bench_c5)):
-            try:
-                breakdown[name] = fn(torch, hkv_amd, stream, gen)
-            except Exception as exc:  # reported, never fatal for the main line
-                breakdown[name] = {"error": repr(exc)}
-            gc.collect()
-            torch.cuda.empty_cache()
+        breakdown.update(run_configs(torch, hkv_amd, stream, gen))
 
     # The dominant operation of the step sets the roofline line.
     if ins_ms >= find_ms:
