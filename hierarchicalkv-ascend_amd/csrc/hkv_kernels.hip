@@ -3,16 +3,19 @@
 // Read-only and idempotent operations (find, find missed, erase, export,
 // size, clear) run one thread per key or per slot.  Every mutating batch
 // operation (insert_or_assign, find_or_insert, insert_and_evict,
-// accum_or_assign, assign_scores) runs in two steps:
-//   1. route: every key atomically appends its batch index to its bucket's
-//      pending list (arrival order);
-//   2. apply: one 16-lane group owns one bucket, sorts the bucket's pending
-//      indices and applies the keys one at a time in increasing batch index.
-// A bucket is therefore only ever written by one group, with no atomics on
-// table memory, and the outcome equals the reference kernel run key by key
-// in batch order (including slot placement and eviction tie-breaks).
-// Buckets that receive more keys than the pending list holds are applied by
-// a second kernel that walks the whole batch in index order.
+// accum_or_assign, assign_scores) is applied as if its keys ran one at a
+// time in increasing batch index, each by the reference kernel's per-key
+// algorithm (slot placement and eviction tie-breaks included):
+//   1. partition: the batch is grouped by partition (256 consecutive
+//      buckets) in batch-chunk order (k_pcount, k_pscan, k_pscatter);
+//   2. apply: one workgroup owns each partition, so no atomic touches table
+//      memory.  k_apply_fast applies a partition key-parallel where that
+//      provably gives the sequential outcome and hands evictions to
+//      k_apply_deferred (a 16-lane group per bucket); k_apply_part takes the
+//      partitions it leaves: duplicate-heavy buckets folded per distinct key,
+//      the rest by a lane-per-bucket walk in batch order.
+// The route/apply kernels (per-bucket pending lists) serve tables and batches
+// the partition pipeline does not cover.
 #include <hip/hip_runtime.h>
 
 #include "hkv_kernels.h"

@@ -108,8 +108,10 @@ int hkv_insert_or_assign(hkv_table* t, uint64_t n, const void* keys,
                          hkv_stream stream, int unique_key,
                          int ignore_evict_strategy);
 
-/* `d_evicted_counter` is accumulated into (not cleared), as in the
- * reference; insert_and_evict throws in hybrid mode. */
+/* As in the reference, the evicted_* buffers hold n records and
+ * `d_evicted_counter` must be 0 at the call: the record count is added to it,
+ * and records are written at positions below n before being compacted into
+ * [0, count).  insert_and_evict fails (runtime_error) in hybrid mode. */
 int hkv_insert_and_evict(hkv_table* t, uint64_t n, const void* keys,
                          const void* values, const uint64_t* scores,
                          void* evicted_keys, void* evicted_values,
