@@ -2442,47 +2442,47 @@ __device__ __forceinline__ uint32_t sel4(uint32_t w0, uint32_t w1, uint32_t w2, 
 // (in the first group only at or after start).  The first two digest matches
 // met before the probe ends are recorded: their keys decide whether the key
 // is present.  A probe the window does not decide goes to the serial lane.
+// After the first EMPTY slot the scan records the next EMPTY slots of the
+// window: a key absent before the call ends its probe at the first of them
+// that no earlier key of the call has taken (digest matches past the first
+// EMPTY slot belong to other keys, since a key always sits before the first
+// EMPTY slot of its probe).
+constexpr uint32_t kMoreEmpty = 1;  // EMPTY slots recorded after the first
+
 struct WinProbe {
-  uint32_t slot;    // first EMPTY slot of the probe (when found)
-  uint32_t c0, c1;  // first two digest matches (kNone: none)
-  uint32_t slot2;   // the next EMPTY slot after `slot` with no digest match
-                    // between them (kNone: none in the window)
-  bool found;       // the probe reached an EMPTY slot
-  bool over;        // more than two digest matches
-  bool done;        // `slot2` is decided
+  uint32_t slot;                // first EMPTY slot of the probe (when found)
+  uint32_t c0, c1;              // first two digest matches (kNone: none)
+  uint32_t more[kMoreEmpty];    // the next EMPTY slots in probe order (kNone: none)
+  uint32_t nmore;
+  bool found;                   // the probe reached an EMPTY slot
+  bool over;                    // more than two digest matches
 };
 
-// One group (digests w, first slot gs) of a probe.  After the first EMPTY
-// slot the scan goes on for the second one: if an earlier key of the call
-// takes the first, the key's probe ends at the second unless a digest match
-// lies between them.
+// One group (digests w, first slot gs) of a probe.
 __device__ __forceinline__ void probe_group(WinProbe& r, uint32_t w, uint32_t gs, uint32_t rep,
                                             uint32_t emask) {
   uint32_t m = eq_bytes4(w, rep);
   uint32_t e = eq_bytes4(w, (uint32_t)kEmptyDigest * 0x01010101u) & emask;
-  if (r.found) {
-    if (m) r.done = true;
-    else if (e) {
-      r.slot2 = gs + __builtin_ctz(e);
-      r.done = true;
+  if (!r.found) {
+    while (m) {
+      const uint32_t p = gs + __builtin_ctz(m);
+      m &= m - 1;
+      if (r.c0 == kNone) r.c0 = p;
+      else if (r.c1 == kNone) r.c1 = p;
+      else r.over = true;
     }
-    return;
-  }
-  while (m) {
-    const uint32_t p = gs + __builtin_ctz(m);
-    m &= m - 1;
-    if (r.c0 == kNone) r.c0 = p;
-    else if (r.c1 == kNone) r.c1 = p;
-    else r.over = true;
-  }
-  if (e) {
+    if (!e) return;
     r.found = true;
     r.slot = gs + __builtin_ctz(e);
-    e &= e - 1;  // later EMPTY slots of the same group (its matches are recorded)
-    if (e) {
-      r.slot2 = gs + __builtin_ctz(e);
-      r.done = true;
-    }
+    e &= e - 1;
+  }
+  while (e && r.nmore < kMoreEmpty) {
+    const uint32_t p = gs + __builtin_ctz(e);
+    e &= e - 1;
+#pragma unroll
+    for (uint32_t j = 0; j < kMoreEmpty; j++)
+      if (j == r.nmore) r.more[j] = p;
+    r.nmore++;
   }
 }
 
@@ -2498,10 +2498,10 @@ __device__ __forceinline__ WinProbe probe_window(u32x4 w0, u32x4 w1, uint32_t st
   const uint32_t emask = empties ? 0xFu : 0u;
   const uint32_t first_mask = ~((1u << (start - a)) - 1u) & emask;
   const uint32_t words[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-  WinProbe r{0, kNone, kNone, kNone, false, false, false};
+  WinProbe r{0, kNone, kNone, {kNone}, 0, false, false};
 #pragma unroll
   for (uint32_t q = 0; q < 8; q++) {
-    if (q < g0 || r.done) continue;
+    if (q < g0 || r.nmore == kMoreEmpty) continue;
     probe_group(r, words[q], (cbase + 4 * q) & (B - 1), rep, q == g0 ? first_mask : emask);
   }
   return r;
@@ -2564,6 +2564,75 @@ __device__ __forceinline__ int probe_serial(const TableView& t, uint64_t base, u
   return -1;
 }
 
+// Metadata records (at most one per slot) and row copies of the entries of a
+// k_apply_fast block whose bucket's serial flag equals `ser` (2: every
+// bucket), by the threads
+// t0 .. t0 + nthr - 1 of the block (whole waves; nthr a multiple of 64).
+// Tasks of different keys name different rows (a superseded write was
+// dropped), except that a forwarded read takes an input row that is only
+// read, so they run in any order.
+template <int U, bool kMovesRows>
+__device__ __forceinline__ void emit_fast(const TableView& t, const ApplyArgs& a, uint32_t m,
+                                          uint64_t part_b0, uint32_t t0, uint32_t nthr,
+                                          uint8_t ser, const uint64_t* s_key,
+                                          const uint32_t* s_idx, const uint64_t* s_sc,
+                                          const uint8_t* s_slot, const uint8_t* s_fl,
+                                          const uint32_t* s_off, const uint32_t* s_cnt,
+                                          const uint8_t* s_isser, uint32_t* s_rows) {
+  const uint32_t B = t.B;
+  for (uint32_t e = t0; e < m; e += nthr) {
+    const uint32_t f = s_fl[e] & kMetaMask;
+    if (!f) continue;
+    const uint64_t k = s_key[e];
+    const uint64_t h = murmur3(k);
+    const uint64_t gb = global_idx(t, h) >> t.bshift;
+    const uint32_t lbk = (uint32_t)(gb % kPartBuckets);
+    if (ser != 2 && s_isser[lbk] != ser) continue;
+    if (e - s_off[lbk] >= s_cnt[lbk]) continue;  // left to k_apply_deferred
+    const uint64_t s = gb * B + s_slot[e];
+    if (f == kMetaKey) {
+      slot_store(t, s, k, s_sc[e]);
+      G(t.digests)[s] = (uint8_t)key_digest(h);
+    } else {
+      slot_score(t, s) = s_sc[e];
+    }
+  }
+  if (!kMovesRows) return;
+  const uint64_t R64 = t.row_bytes;
+  for (uint32_t e0 = 0; e0 < m; e0 += nthr) {
+    const uint32_t e = e0 + t0;
+    uint64_t src = 0, dst = 0;
+    uint32_t tk = e < m ? (s_fl[e] & kTkMask) : 0u;
+    uint64_t gb = 0;
+    if (tk) {
+      gb = bucket_of(t, s_key[e]);
+      const uint32_t lbk = (uint32_t)(gb % kPartBuckets);
+      if ((ser != 2 && s_isser[lbk] != ser) || e - s_off[lbk] >= s_cnt[lbk]) tk = 0;
+    }
+    if (tk) {
+      const uint64_t i = s_idx[e];
+      const uint32_t sl = s_slot[e];
+      const uint64_t trow = (uint64_t)(uintptr_t)row_ptr(t, gb, sl);
+      if (tk == kTkIn) {
+        src = (uint64_t)(uintptr_t)(a.in_values + i * R64);
+        dst = trow;
+      } else if (tk == kTkOut) {
+        src = trow;
+        dst = (uint64_t)(uintptr_t)(a.io_values + i * R64);
+      } else {
+        // The latest earlier key of the bucket whose input row was queued
+        // for this slot.
+        uint32_t xs = e;
+        for (uint32_t x = s_off[gb % kPartBuckets]; x < e; x++)
+          if (s_slot[x] == sl && (s_fl[x] & kTkMask) == kTkIn) xs = x;
+        src = (uint64_t)(uintptr_t)(a.io_values + (uint64_t)s_idx[xs] * R64);
+        dst = (uint64_t)(uintptr_t)(a.io_values + i * R64);
+      }
+    }
+    wave_copy_pairs_q<U, 4>(src, dst, t.row_bytes, s_rows);
+  }
+}
+
 template <int OP, int U>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_apply_fast(TableView t, ApplyArgs a, PartScratch ps) {
   static_assert(OP != OP_ACCUM_OR_ASSIGN, "accumulation runs in k_apply_part");
@@ -2578,17 +2647,18 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
   __shared__ uint32_t s_idx[kFastLds];    // batch index
   __shared__ uint8_t s_slot[kFastLds];    // slot of the outcome (kNoSlot: none)
   __shared__ uint8_t s_fl[kFastLds];      // outcome, metadata record and row task
-  __shared__ uint8_t s_slot2[kFastLds];   // second EMPTY slot of the probe (kNoSlot: none)
+  __shared__ uint8_t s_more[kMoreEmpty][kFastLds];  // next EMPTY slots of the window (kNoSlot: none)
   __shared__ uint32_t s_cnt[kPartBuckets];  // keys per bucket, fill pointers, then stops
   __shared__ uint32_t s_off[kPartBuckets + 1];  // first entry of each bucket
   __shared__ uint8_t s_bsz[kPartBuckets];   // bucket sizes before the call
-  static_assert(sizeof(uint64_t) * kFastLds >= sizeof(uint32_t) * kBlock, "row lists");
-  // Row lists of the copies, in the score array (no longer read by then).
-  uint32_t(*s_rows)[64] = reinterpret_cast<uint32_t(*)[64]>(s_sc);
+  // Row lists of the copies (own storage: copies run while the serial lanes
+  // still read and write the scores).
+  __shared__ uint32_t s_rows[kBlock / 64][64];
   __shared__ uint32_t s_wsum[kBlock / 64];
   __shared__ uint32_t s_big;
   __shared__ uint32_t s_nrec, s_npool;  // hand-over records and pool entries of the block
   __shared__ uint8_t s_serial[kPartBuckets];  // buckets left to the serial lanes
+  __shared__ uint8_t s_isser[kPartBuckets];   // 1 for those buckets
   __shared__ uint32_t s_nser;
   __shared__ uint32_t s_rbase, s_pbase;
   const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -2600,7 +2670,6 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
   }
   if (m == 0) return;
   const uint32_t B = t.B;
-  const uint32_t R = t.row_bytes;
   const uint64_t part_b0 = (uint64_t)p * kPartBuckets;
   const bool has_in = a.in_scores != nullptr;
   const bool old_for_hit = a.sc.strategy == kLfu || a.sc.strategy == kEpochLfu;
@@ -2714,7 +2783,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
 #pragma unroll
     for (uint32_t q = 0; q < kPer; q++) {
       const uint32_t e = tid + q * kBlock;
-      wp[q] = WinProbe{0, kNone, kNone, kNone, false, true, true};
+      wp[q] = WinProbe{0, kNone, kNone, {kNone}, 0, false, true};
       if (e < m) {
         const uint32_t d = key_digest(murmur3(s_key[e]));
         const uint32_t lbk = (uint32_t)((gi[q] >> t.bshift) % kPartBuckets);
@@ -2766,7 +2835,9 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
         }
       }
       s_slot[e] = slot;
-      s_slot2[e] = wp[q].slot2 != kNone ? (uint8_t)wp[q].slot2 : kNoSlot;
+#pragma unroll
+      for (uint32_t j = 0; j < kMoreEmpty; j++)
+        s_more[j][e] = wp[q].more[j] != kNone ? (uint8_t)wp[q].more[j] : kNoSlot;
       s_fl[e] = fl;
       if (fl != kResSlow) s_sc[e] = sc;
     }
@@ -2808,6 +2879,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
   {
     const uint32_t bk = tid;
     const uint32_t lo = s_off[bk], hi = s_off[bk + 1], c = hi - lo;
+    s_isser[bk] = s_cnt[bk] < c ? 1 : 0;
     if (s_cnt[bk] < c) {
       s_serial[atomicAdd(&s_nser, 1u)] = (uint8_t)bk;
     } else if (lo < hi) {
@@ -2822,7 +2894,15 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
     }
   }
   lds_barrier();
-  if (tid < s_nser) {
+  // The waves that hold serial lanes run them; meanwhile the other waves write
+  // the records and copy the rows of the buckets the parallel pass applied
+  // whole (different buckets, so neither touches what the other reads).
+  const uint32_t ns_w = (s_nser + 63) / 64;
+  if (wv >= ns_w) {
+    emit_fast<U, moves_rows>(t, a, m, part_b0, (wv - ns_w) * 64 + lane, (kBlock / 64 - ns_w) * 64,
+                             0, s_key, s_idx, s_sc, s_slot, s_fl, s_off, s_cnt, s_isser,
+                             s_rows[wv]);
+  } else if (tid < s_nser) {
     const uint32_t bk = s_serial[tid];
     const uint64_t b = part_b0 + bk;
     const uint32_t lo = s_off[bk], hi = s_off[bk + 1], c = hi - lo;
@@ -2876,19 +2956,29 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
         break;
       }
       if (!known && pres == kResNew) {
-        // If an earlier key took the first EMPTY slot, the probe goes on to
-        // the second (recorded when no digest match lies between them).
-        const uint32_t ts = s_slot[e], ts2 = s_slot2[e];
-        bool taken = false, taken2 = false;
+        // The probe ends at the first of the recorded EMPTY slots (the first
+        // one, then the window's next ones) that no earlier key took.
+        uint32_t cand[1 + kMoreEmpty];
+        bool taken[1 + kMoreEmpty];
+        cand[0] = s_slot[e];
+#pragma unroll
+        for (uint32_t j = 0; j < kMoreEmpty; j++) cand[1 + j] = s_more[j][e];
+#pragma unroll
+        for (uint32_t j = 0; j <= kMoreEmpty; j++) taken[j] = false;
         for (uint32_t x = lo; x < e; x++) {
           if ((s_fl[x] & kResMask) == kResNew) {
-            taken |= s_slot[x] == ts;
-            taken2 |= s_slot[x] == ts2;
+            const uint32_t sx = s_slot[x];
+#pragma unroll
+            for (uint32_t j = 0; j <= kMoreEmpty; j++) taken[j] |= sx == cand[j];
           }
         }
-        if (!taken || (ts2 != kNoSlot && !taken2)) {
-          sl = (int)(taken ? ts2 : ts);
-          known = true;
+#pragma unroll
+        for (uint32_t j = 0; j <= kMoreEmpty; j++) {
+          if (!known && cand[j] != kNoSlot && !taken[j]) {
+            sl = (int)cand[j];
+            known = true;
+          }
+          if (cand[j] == kNoSlot) break;
         }
       }
       if (!known)
@@ -2968,26 +3058,10 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
   }
   lds_barrier();
 
-  /* W. Metadata of the applied keys: at most one record per slot. */
-#pragma unroll
-  for (uint32_t q = 0; q < kPer; q++) {
-    const uint32_t e = tid + q * kBlock;
-    if (e >= m) continue;
-    const uint32_t f = s_fl[e] & kMetaMask;
-    if (!f) continue;
-    const uint64_t k = s_key[e];
-    const uint64_t h = murmur3(k);
-    const uint64_t gb = global_idx(t, h) >> t.bshift;
-    const uint32_t lbk = (uint32_t)(gb % kPartBuckets);
-    if (e - s_off[lbk] >= s_cnt[lbk]) continue;  // left to k_apply_deferred
-    const uint64_t s = gb * B + s_slot[e];
-    if (f == kMetaKey) {
-      slot_store(t, s, k, s_sc[e]);
-      G(t.digests)[s] = (uint8_t)key_digest(h);
-    } else {
-      slot_score(t, s) = s_sc[e];
-    }
-  }
+  /* W. Records and rows of the serial buckets; also of the others when
+        every wave held serial lanes (none was free to emit them above). */
+  emit_fast<U, moves_rows>(t, a, m, part_b0, tid, kBlock, ns_w == kBlock / 64 ? 2 : 1, s_key,
+                           s_idx, s_sc, s_slot, s_fl, s_off, s_cnt, s_isser, s_rows[wv]);
 #pragma unroll
   for (int d = 32; d > 0; d >>= 1) added += __shfl_xor(added, d, 64);
   if (lane == 0) s_wsum[wv] = added;
@@ -3023,44 +3097,6 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
     }
   }
 
-  // Row copies of the block's tasks.  Tasks of different keys name different
-  // rows (a superseded write was dropped above), except that a forwarded
-  // read takes an input row that is only read, so they run in any order.
-  if (moves_rows) {
-    const uint64_t R64 = R;
-    for (uint32_t e0 = 0; e0 < m; e0 += kBlock) {
-      const uint32_t e = e0 + tid;
-      uint64_t src = 0, dst = 0;
-      uint32_t tk = e < m ? (s_fl[e] & kTkMask) : 0u;
-      uint64_t gb = 0;
-      if (tk) {
-        gb = bucket_of(t, s_key[e]);
-        const uint32_t lbk = (uint32_t)(gb % kPartBuckets);
-        if (e - s_off[lbk] >= s_cnt[lbk]) tk = 0;
-      }
-      if (tk) {
-        const uint64_t i = s_idx[e];
-        const uint32_t sl = s_slot[e];
-        const uint64_t trow = (uint64_t)(uintptr_t)row_ptr(t, gb, sl);
-        if (tk == kTkIn) {
-          src = (uint64_t)(uintptr_t)(a.in_values + i * R64);
-          dst = trow;
-        } else if (tk == kTkOut) {
-          src = trow;
-          dst = (uint64_t)(uintptr_t)(a.io_values + i * R64);
-        } else {
-          // The latest earlier key of the bucket whose input row was
-          // queued for this slot.
-          uint32_t xs = e;
-          for (uint32_t x = s_off[gb % kPartBuckets]; x < e; x++)
-            if (s_slot[x] == sl && (s_fl[x] & kTkMask) == kTkIn) xs = x;
-          src = (uint64_t)(uintptr_t)(a.io_values + (uint64_t)s_idx[xs] * R64);
-          dst = (uint64_t)(uintptr_t)(a.io_values + i * R64);
-        }
-      }
-      wave_copy_pairs_q<U, 4>(src, dst, R, s_rows[wv]);
-    }
-  }
 }
 
 // One 16-lane group per bucket handed over by k_apply_fast, which applied
