@@ -488,13 +488,12 @@ __device__ __forceinline__ uint64_t ev_slot(const ApplyArgs& a, uint64_t i, uint
 // insert_or_assign_kernel.h:76-303 (unique keys) and find_and_lock
 // (find_utils.h:94-227) with its callers (non-unique keys and accum).
 template <int OP, int U>
-__device__ __forceinline__ void apply_key(const TableView& t, Bucket16& S, const ApplyArgs& a,
-                                          uint64_t i, uint64_t k) {
+__device__ __forceinline__ void apply_key_in(const TableView& t, Bucket16& S, const ApplyArgs& a,
+                                             uint64_t i, uint64_t k, uint64_t in) {
   constexpr int SPL = 8;
   const uint32_t B = t.B;
   const uint32_t l = S.l;
   const bool has_in = a.in_scores != nullptr;
-  const uint64_t in = has_in ? G(a.in_scores)[i] : 0;
   const uint64_t h = murmur3(k);
   const uint64_t gi = global_idx(t, h);
   const uint32_t start = (uint32_t)(gi & (B - 1));
@@ -662,6 +661,14 @@ __device__ __forceinline__ void apply_key(const TableView& t, Bucket16& S, const
       rec_set(S.key, jj, k);
     }
   }
+}
+
+// apply_key_in with the key's input score loaded here.
+template <int OP, int U>
+__device__ __forceinline__ void apply_key(const TableView& t, Bucket16& S, const ApplyArgs& a,
+                                          uint64_t i, uint64_t k) {
+  const uint64_t in = a.in_scores ? G(a.in_scores)[i] : 0;
+  apply_key_in<OP, U>(t, S, a, i, k, in);
 }
 
 __device__ __forceinline__ void bucket_finish(const TableView& t, Bucket16& S) {
@@ -3114,11 +3121,25 @@ __global__ __launch_bounds__(kBlock) void k_apply_deferred(TableView t, ApplyArg
     gptr<const uint32_t> rec = G(ps.drec) + 4 * r;
     const uint64_t b = rec[0];
     const uint32_t c = rec[1], st = rec[2], po = rec[3];
+    // The first 16 keys left, one per lane, and their input scores, load
+    // beside the bucket instead of one dependent pair per step.
+    u64x2 mine;
+    mine.x = 0;
+    mine.y = 0;
+    if (st + gl < c) mine = pool[po + st + gl];
     Bucket16 S;
     bucket_load(t, S, b, gl);
+    const uint64_t mine_in = (st + gl < c && a.in_scores) ? G(a.in_scores)[mine.y] : 0;
     for (uint32_t step = st; step < c; step++) {
-      const u64x2 v = pool[po + step];
-      apply_key<OP, U>(t, S, a, v.y, v.x);
+      const uint32_t j = step - st;  // uniform in the group
+      if (j < 16) {
+        const uint64_t k = shfl_u64(mine.x, (int)j, 16);
+        const uint64_t i = shfl_u64(mine.y, (int)j, 16);
+        apply_key_in<OP, U>(t, S, a, i, k, shfl_u64(mine_in, (int)j, 16));
+      } else {
+        const u64x2 v = pool[po + step];
+        apply_key<OP, U>(t, S, a, v.y, v.x);
+      }
     }
     bucket_finish(t, S);
   }
