@@ -2431,6 +2431,7 @@ constexpr uint8_t kMetaScore = 2;   // present key: score written
 constexpr uint8_t kMetaMask = 3;
 constexpr uint8_t kTkIn = 1 << 2;   // input row -> table row
 constexpr uint8_t kTkOut = 2 << 2;  // table row -> output row
+constexpr uint8_t kTkAcc = kTkOut;  // accum_or_assign: input delta added into the table row
 constexpr uint8_t kTkFwd = 3 << 2;  // input row of the earlier key that wrote the slot -> output row
 constexpr uint8_t kTkMask = 3 << 2;
 constexpr uint8_t kResNew = 1 << 4;   // absent; the slot is the probe's first EMPTY slot
@@ -2571,6 +2572,66 @@ __device__ __forceinline__ int probe_serial(const TableView& t, uint64_t base, u
   return -1;
 }
 
+// Element-wise dst += src over one U-byte unit, for the value types
+// accum_or_assign supports (f32, i32, i64/u64), in the reference's order
+// (`val = delta; val += dst`, accum_or_assign_kernel.h:41-49).
+template <typename T>
+__device__ __forceinline__ T add_unit(T row, T delta, int vt) {
+  constexpr int W = sizeof(T) / 4;  // 32-bit words in the unit (>= 1)
+  uint32_t r[W > 0 ? W : 1], d[W > 0 ? W : 1];
+  __builtin_memcpy(r, &row, sizeof(T));
+  __builtin_memcpy(d, &delta, sizeof(T));
+  if (vt == 0) {  // f32
+#pragma unroll
+    for (int j = 0; j < W; j++) {
+      float v = __uint_as_float(d[j]);
+      v += __uint_as_float(r[j]);
+      r[j] = __float_as_uint(v);
+    }
+  } else if (vt == 8) {  // i32
+#pragma unroll
+    for (int j = 0; j < W; j++) r[j] = (uint32_t)((int32_t)d[j] + (int32_t)r[j]);
+  } else {  // i64 / u64
+#pragma unroll
+    for (int j = 0; j + 1 < W; j += 2) {
+      const uint64_t v = (((uint64_t)d[j + 1] << 32) | d[j]) + (((uint64_t)r[j + 1] << 32) | r[j]);
+      r[j] = (uint32_t)v;
+      r[j + 1] = (uint32_t)(v >> 32);
+    }
+  }
+  T out;
+  __builtin_memcpy(&out, r, sizeof(T));
+  return out;
+}
+
+// Wave-cooperative accumulation: the lane with dst != 0 has its row of
+// deltas (src) added into the table row dst; lpr lanes per row, one unit each.
+// Different lanes name different table rows.
+template <int U>
+__device__ __forceinline__ void wave_accum_pairs(uint64_t src, uint64_t dst, uint32_t row_bytes,
+                                                 int vt, uint32_t* s_rows) {
+  using T = typename UnitT<U>::T;
+  const uint32_t lane = threadIdx.x & 63;
+  const uint64_t hm = __ballot(dst != 0);
+  if (!hm) return;
+  if (dst) s_rows[__popcll(hm & ((1ull << lane) - 1))] = lane;
+  __builtin_amdgcn_wave_barrier();
+  const uint32_t rows = __popcll(hm);
+  const uint32_t units = row_bytes / U;
+  uint32_t lpr = 64;
+  while (lpr > 1 && lpr / 2 >= units) lpr >>= 1;
+  const uint32_t rpi = 64 / lpr, sub = lane % lpr;
+  for (uint32_t r0 = 0; r0 < rows; r0 += rpi) {
+    const uint32_t r = r0 + lane / lpr;
+    const uint32_t l = s_rows[r < rows ? r : 0];
+    gptr<const T> sp = G<const T>((uintptr_t)shfl_u64(src, (int)l, 64));
+    gptr<T> dp = G<T>((uintptr_t)shfl_u64(dst, (int)l, 64));
+    if (r < rows)
+      for (uint32_t u = sub; u < units; u += lpr) dp[u] = add_unit<T>(dp[u], sp[u], vt);
+  }
+  __builtin_amdgcn_wave_barrier();
+}
+
 // Metadata records (at most one per slot) and row copies of the entries of a
 // k_apply_fast block whose bucket's serial flag equals `ser` (2: every
 // bucket), by the threads
@@ -2578,7 +2639,7 @@ __device__ __forceinline__ int probe_serial(const TableView& t, uint64_t base, u
 // Tasks of different keys name different rows (a superseded write was
 // dropped), except that a forwarded read takes an input row that is only
 // read, so they run in any order.
-template <int U, bool kMovesRows>
+template <int OP, int U, bool kMovesRows>
 __device__ __forceinline__ void emit_fast(const TableView& t, const ApplyArgs& a, uint32_t m,
                                           uint64_t part_b0, uint32_t t0, uint32_t nthr,
                                           uint8_t ser, const uint64_t* s_key,
@@ -2608,7 +2669,7 @@ __device__ __forceinline__ void emit_fast(const TableView& t, const ApplyArgs& a
   const uint64_t R64 = t.row_bytes;
   for (uint32_t e0 = 0; e0 < m; e0 += nthr) {
     const uint32_t e = e0 + t0;
-    uint64_t src = 0, dst = 0;
+    uint64_t src = 0, dst = 0, asrc = 0, adst = 0;
     uint32_t tk = e < m ? (s_fl[e] & kTkMask) : 0u;
     uint64_t gb = 0;
     if (tk) {
@@ -2623,6 +2684,9 @@ __device__ __forceinline__ void emit_fast(const TableView& t, const ApplyArgs& a
       if (tk == kTkIn) {
         src = (uint64_t)(uintptr_t)(a.in_values + i * R64);
         dst = trow;
+      } else if (tk == kTkOut && OP == OP_ACCUM_OR_ASSIGN) {
+        asrc = (uint64_t)(uintptr_t)(a.in_values + i * R64);  // kTkAcc
+        adst = trow;
       } else if (tk == kTkOut) {
         src = trow;
         dst = (uint64_t)(uintptr_t)(a.io_values + i * R64);
@@ -2637,12 +2701,12 @@ __device__ __forceinline__ void emit_fast(const TableView& t, const ApplyArgs& a
       }
     }
     wave_copy_pairs_q<U, 4>(src, dst, t.row_bytes, s_rows);
+    if (OP == OP_ACCUM_OR_ASSIGN) wave_accum_pairs<U>(asrc, adst, t.row_bytes, a.value_type, s_rows);
   }
 }
 
 template <int OP, int U>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_apply_fast(TableView t, ApplyArgs a, PartScratch ps) {
-  static_assert(OP != OP_ACCUM_OR_ASSIGN, "accumulation runs in k_apply_part");
   constexpr uint32_t kPer = (kFastLds + kBlock - 1) / kBlock;  // entries per thread
   constexpr bool may_insert = OP != OP_ASSIGN_SCORES;
   constexpr bool moves_rows = OP != OP_ASSIGN_SCORES;
@@ -2785,6 +2849,14 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
         w1[q] = drow[((a4 >> 4) + 1) & (B / 16 - 1)];
       }
     }
+    // accum_or_assign: accumulate (flag set) applies to present keys only,
+    // assign (flag clear) to absent keys only; the other cases are no-ops.
+    bool flag[kPer];
+#pragma unroll
+    for (uint32_t q = 0; q < kPer; q++) {
+      const uint32_t e = tid + q * kBlock;
+      flag[q] = OP == OP_ACCUM_OR_ASSIGN && e < m && G(a.accum_flags)[s_idx[e]] != 0;
+    }
     WinProbe wp[kPer];
     uint64_t k0[kPer], k1[kPer];  // keys at the first two digest matches
 #pragma unroll
@@ -2823,7 +2895,11 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
       if (hit0 || hit1 || (wp[q].found && !wp[q].over)) {
         const uint64_t des = score_desired(a.sc, has_in, in);
         bool w;
-        if (hit0 || hit1) {
+        if ((hit0 || hit1) && OP == OP_ACCUM_OR_ASSIGN && !flag[q]) {
+          fl = 0;  // present, assign requested: a no-op
+        } else if (!(hit0 || hit1) && OP == OP_ACCUM_OR_ASSIGN && flag[q]) {
+          fl = 0;  // absent, accumulate requested: a no-op
+        } else if (hit0 || hit1) {
           const bool first = hit0;
           slot = (uint8_t)(first ? wp[q].c0 : wp[q].c1);
           const uint64_t old =
@@ -2832,7 +2908,8 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
                                                      : score_hit(a.sc, has_in, in, des, old, &w);
           fl = kResDup | (w ? kMetaScore : 0);
           sc = ns;
-          if (moves_rows) fl |= reads_rows ? kTkOut : kTkIn;
+          if (OP == OP_ACCUM_OR_ASSIGN) fl |= kTkAcc;
+          else if (moves_rows) fl |= reads_rows ? kTkOut : kTkIn;
         } else if (!may_insert) {
           fl = 0;  // assign_scores: absent keys are a no-op
         } else if (!old_for_new) {
@@ -2906,7 +2983,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
   // whole (different buckets, so neither touches what the other reads).
   const uint32_t ns_w = (s_nser + 63) / 64;
   if (wv >= ns_w) {
-    emit_fast<U, moves_rows>(t, a, m, part_b0, (wv - ns_w) * 64 + lane, (kBlock / 64 - ns_w) * 64,
+    emit_fast<OP, U, moves_rows>(t, a, m, part_b0, (wv - ns_w) * 64 + lane, (kBlock / 64 - ns_w) * 64,
                              0, s_key, s_idx, s_sc, s_slot, s_fl, s_off, s_cnt, s_isser,
                              s_rows[wv]);
   } else if (tid < s_nser) {
@@ -2996,9 +3073,23 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
         stop = r;
         break;
       }
+      if (OP == OP_ACCUM_OR_ASSIGN && sl >= 0 && dup) {
+        // An accumulation onto a row an earlier key of the call wrote or
+        // accumulated runs after that task: the eviction kernel applies the
+        // rest of the bucket in order, after this kernel's row tasks.
+        bool chain = false;
+        for (uint32_t x = lo; x < e; x++)
+          chain |= s_slot[x] == (uint32_t)sl && (s_fl[x] & kTkMask) != 0;
+        if (chain && G(a.accum_flags)[i] != 0) {
+          stop = r;
+          break;
+        }
+      }
       stop = r + 1;
       uint8_t fl = 0;
-      if (sl < 0 || (!may_insert && !dup)) {  // assign_scores: absent
+      if (sl < 0 || (!may_insert && !dup) ||
+          (OP == OP_ACCUM_OR_ASSIGN && (G(a.accum_flags)[i] != 0) != (dup != 0))) {
+        // assign_scores: absent; accum_or_assign: the flag does not match
         s_slot[e] = kNoSlot;
         s_fl[e] = 0;
         continue;
@@ -3028,7 +3119,9 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
             s_sc[e] = ns;
           }
         }
-        if (moves_rows) {
+        if (OP == OP_ACCUM_OR_ASSIGN) {
+          fl |= kTkAcc;
+        } else if (moves_rows) {
           if (reads_rows) {
             fl |= xin != kNone ? kTkFwd : kTkOut;
           } else {
@@ -3067,7 +3160,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
 
   /* W. Records and rows of the serial buckets; also of the others when
         every wave held serial lanes (none was free to emit them above). */
-  emit_fast<U, moves_rows>(t, a, m, part_b0, tid, kBlock, ns_w == kBlock / 64 ? 2 : 1, s_key,
+  emit_fast<OP, U, moves_rows>(t, a, m, part_b0, tid, kBlock, ns_w == kBlock / 64 ? 2 : 1, s_key,
                            s_idx, s_sc, s_slot, s_fl, s_off, s_cnt, s_isser, s_rows[wv]);
 #pragma unroll
   for (int d = 32; d > 0; d >>= 1) added += __shfl_xor(added, d, 64);
@@ -3473,7 +3566,7 @@ static void apply_part_op(const TableView& t, const ApplyArgs& a, const PartScra
   hipLaunchKernelGGL(k_pscan, dim3((ps.np + 15) / 16), dim3(1024), 0, s, ps);
   hipLaunchKernelGGL(k_pscatter, dim3(ps.chunks), dim3(kBlock), lds, s, t, a.keys, a.n, ps);
   const dim3 g(ps.np), b(kBlock);
-  constexpr bool fast = OP != OP_ACCUM_OR_ASSIGN;
+  constexpr bool fast = true;
   // After the single-run kernel, the eviction path and the multi-run kernel
   // walk device-side lists that are usually empty: small grids.
   const dim3 gd(grid_for(a.n * 16, kBlock, 2048));

@@ -205,6 +205,32 @@ def test_accum_or_assign():
         p.assert_same_state()
 
 
+@pytest.mark.parametrize("strategy", [O.CUSTOMIZED, O.LFU, O.LRU])
+def test_accum_or_assign_repeated_keys(strategy):
+    """accum_or_assign with keys repeated in a batch and mixed flags: an
+    assign followed by accumulations of the same key, accumulations of one
+    present key in a row, no-op flag mismatches, into a table that fills and
+    evicts; i32 rows check the integer accumulation."""
+    rng = np.random.default_rng(117)
+    for vt, dt in (("f32", np.float32), ("i32", np.int32)):
+        p = Pair(1 << 12, dim=8, strategy=strategy, vt=vt)
+        pool = uniform_keys(rng, 3000)
+        base = pool[:1500]
+        init = (rand_vals(rng, base.size, 8) if vt == "f32"
+                else rng.integers(-10**6, 10**6, (base.size, 8)).astype(np.int32))  # no overflow
+        p.insert_or_assign(base, init, None if strategy == O.LRU else
+                           rng.integers(0, 1000, base.size, dtype=np.uint64))
+        for b in range(5):
+            q = rng.choice(pool, 4000)
+            flags = rng.integers(0, 2, q.size).astype(np.uint8)
+            deltas = (rng.uniform(-0.01, 0.01, (q.size, 8)).astype(np.float32) if vt == "f32"
+                      else rng.integers(-1000, 1000, (q.size, 8)).astype(np.int32))
+            p.accum_or_assign(q, deltas, flags,
+                              None if strategy == O.LRU else
+                              rng.integers(0, 1000, q.size, dtype=np.uint64), clock=50 + b)
+            p.assert_same_state()
+
+
 def test_assign_scores():
     rng = np.random.default_rng(110)
     p = Pair(1 << 12, dim=4, strategy=O.LFU)
