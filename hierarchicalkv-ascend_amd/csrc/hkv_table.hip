@@ -787,6 +787,153 @@ int hkv_reserve(hkv_table* t, uint64_t new_capacity, hkv_stream stream) {
   });
 }
 
+namespace {
+
+// Host and device buffers of one save/load chunk.
+struct KvChunk {
+  uint64_t* h_keys = nullptr;
+  uint64_t* h_scores = nullptr;
+  uint8_t* h_values = nullptr;
+  uint64_t* d_keys = nullptr;
+  uint64_t* d_scores = nullptr;
+  uint8_t* d_values = nullptr;
+  uint64_t* d_count = nullptr;
+  KvChunk(uint64_t n, uint64_t row) {
+    hip_check(hipHostMalloc(&h_keys, n * 8, hipHostMallocDefault), "hipHostMalloc(kv keys)");
+    hip_check(hipHostMalloc(&h_scores, n * 8, hipHostMallocDefault), "hipHostMalloc(kv scores)");
+    hip_check(hipHostMalloc(&h_values, n * row, hipHostMallocDefault), "hipHostMalloc(kv rows)");
+    hip_check(hipMalloc(&d_keys, n * 8), "hipMalloc(kv keys)");
+    hip_check(hipMalloc(&d_scores, n * 8), "hipMalloc(kv scores)");
+    hip_check(hipMalloc(&d_values, n * row), "hipMalloc(kv rows)");
+    hip_check(hipMalloc(&d_count, 8), "hipMalloc(kv count)");
+  }
+  ~KvChunk() {
+    (void)hipHostFree(h_keys);
+    (void)hipHostFree(h_scores);
+    (void)hipHostFree(h_values);
+    (void)hipFree(d_keys);
+    (void)hipFree(d_scores);
+    (void)hipFree(d_values);
+    (void)hipFree(d_count);
+  }
+};
+
+uint64_t kv_chunk_records(const hkv_table* t, uint64_t max_workspace_size) {
+  const uint64_t tuple = 8 + 8 + t->row;  // key + score + row
+  if (max_workspace_size < tuple)
+    fail(HKV_ERR_INVALID,
+         "max_workspace_size is smaller than a single key + score + value tuple");
+  return max_workspace_size / tuple;
+}
+
+void ok_or_throw(int rc) {
+  if (rc != HKV_OK) throw HkvError{rc, g_last_error};
+}
+
+}  // namespace
+
+int hkv_save(hkv_table* t, hkv_kv_write_fn write, void* ctx, uint64_t max_workspace_size,
+             hkv_stream stream, uint64_t* count) {
+  return guarded([&] {
+    need_table(t);
+    if (!write || !count) fail(HKV_ERR_INVALID, "write and count must not be null");
+    const hipStream_t s = S(stream);
+    const uint64_t total = t->C;
+    const uint64_t n = std::min(kv_chunk_records(t, max_workspace_size), total);
+    KvChunk c(n, t->row);
+    uint64_t written = 0;
+    for (uint64_t i = 0; i < total; i += n) {
+      const uint64_t m = std::min(total - i, n);
+      ok_or_throw(hkv_export_batch(t, m, i, c.d_count, c.d_keys, c.d_values, c.d_scores, stream));
+      uint64_t got = 0;
+      hip_check(hipMemcpyAsync(&got, c.d_count, 8, hipMemcpyDeviceToHost, s), "hipMemcpy(count)");
+      hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
+      if (got == 0) continue;
+      hip_check(hipMemcpyAsync(c.h_keys, c.d_keys, got * 8, hipMemcpyDeviceToHost, s), "hipMemcpy");
+      hip_check(hipMemcpyAsync(c.h_scores, c.d_scores, got * 8, hipMemcpyDeviceToHost, s),
+                "hipMemcpy");
+      hip_check(hipMemcpyAsync(c.h_values, c.d_values, got * t->row, hipMemcpyDeviceToHost, s),
+                "hipMemcpy");
+      hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
+      write(ctx, got, t->row, c.h_keys, c.h_values, c.h_scores);
+      written += got;
+    }
+    *count = written;
+  });
+}
+
+int hkv_load(hkv_table* t, hkv_kv_read_fn read, void* ctx, uint64_t max_workspace_size,
+             hkv_stream stream, uint64_t* count) {
+  return guarded([&] {
+    need_table(t);
+    if (!read || !count) fail(HKV_ERR_INVALID, "read and count must not be null");
+    const hipStream_t s = S(stream);
+    const uint64_t n = kv_chunk_records(t, max_workspace_size);
+    KvChunk c(n, t->row);
+    uint64_t loaded = 0;
+    uint64_t got = read(ctx, n, t->row, c.h_keys, c.h_values, c.h_scores);
+    while (got > 0) {
+      hip_check(hipMemcpyAsync(c.d_keys, c.h_keys, got * 8, hipMemcpyHostToDevice, s), "hipMemcpy");
+      hip_check(hipMemcpyAsync(c.d_scores, c.h_scores, got * 8, hipMemcpyHostToDevice, s),
+                "hipMemcpy");
+      hip_check(hipMemcpyAsync(c.d_values, c.h_values, got * t->row, hipMemcpyHostToDevice, s),
+                "hipMemcpy");
+      t->epoch = kIgnoredEpoch;  // include/hkv_hashtable.h:3182
+      ok_or_throw(hkv_insert_or_assign(t, got, c.d_keys, c.d_values, c.d_scores, stream, 1, 1));
+      loaded += got;
+      hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
+      got = read(ctx, n, t->row, c.h_keys, c.h_values, c.h_scores);
+    }
+    *count = loaded;
+  });
+}
+
+struct hkv_local_kv_file {
+  FILE* keys = nullptr;
+  FILE* values = nullptr;
+  FILE* scores = nullptr;
+};
+
+hkv_local_kv_file* hkv_local_kv_file_open(const char* keys_path, const char* values_path,
+                                          const char* scores_path, const char* mode) {
+  if (!keys_path || !values_path || !scores_path || !mode) return nullptr;
+  auto* f = new hkv_local_kv_file();
+  f->keys = fopen(keys_path, mode);
+  f->values = f->keys ? fopen(values_path, mode) : nullptr;
+  f->scores = f->values ? fopen(scores_path, mode) : nullptr;
+  if (!f->scores) {
+    hkv_local_kv_file_close(f);
+    return nullptr;
+  }
+  return f;
+}
+
+void hkv_local_kv_file_close(hkv_local_kv_file* f) {
+  if (!f) return;
+  if (f->keys) fclose(f->keys);
+  if (f->values) fclose(f->values);
+  if (f->scores) fclose(f->scores);
+  delete f;
+}
+
+uint64_t hkv_local_kv_file_write(void* fp, uint64_t n, uint64_t row_bytes, const void* keys,
+                                 const void* values, const uint64_t* scores) {
+  auto* f = static_cast<hkv_local_kv_file*>(fp);
+  const size_t nk = fwrite(keys, 8, n, f->keys);
+  const size_t nv = fwrite(values, row_bytes, n, f->values);
+  const size_t ns = fwrite(scores, 8, n, f->scores);
+  return (nk == nv && nk == ns) ? nk : 0;
+}
+
+uint64_t hkv_local_kv_file_read(void* fp, uint64_t n, uint64_t row_bytes, void* keys,
+                                void* values, uint64_t* scores) {
+  auto* f = static_cast<hkv_local_kv_file*>(fp);
+  const size_t nk = fread(keys, 8, n, f->keys);
+  const size_t nv = fread(values, row_bytes, n, f->values);
+  const size_t ns = fread(scores, 8, n, f->scores);
+  return (nk == nv && nk == ns) ? nk : 0;
+}
+
 int hkv_set_global_epoch(hkv_table* t, uint64_t epoch) {
   return guarded([&] {
     need_table(t);

@@ -117,10 +117,21 @@ _SIGS = {
     "hkv_last_error": [],
     "hkv_set_lru_clock": [_vp, _u64, _i32],
     "hkv_live_count": [_vp, _vp, ctypes.POINTER(_u64)],
+    "hkv_save": [_vp, _vp, _vp, _u64, _vp, ctypes.POINTER(_u64)],
+    "hkv_load": [_vp, _vp, _vp, _u64, _vp, ctypes.POINTER(_u64)],
+    "hkv_local_kv_file_open": [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p,
+                               ctypes.c_char_p],
+    "hkv_local_kv_file_close": [_vp],
+    "hkv_local_kv_file_write": [_vp, _u64, _u64, _vp, _vp, _vp],
+    "hkv_local_kv_file_read": [_vp, _u64, _u64, _vp, _vp, _vp],
 }
+# Callback types of hkv_save / hkv_load (a key-value file's write and read).
+_KV_FN = ctypes.CFUNCTYPE(_u64, _vp, _u64, _u64, _vp, _vp, _vp)
 _RESTYPES = {"hkv_options_default": None, "hkv_capacity": _u64, "hkv_dim": _u64,
              "hkv_max_bucket_size": _u64, "hkv_bucket_count": _u64,
-             "hkv_last_error": ctypes.c_char_p}
+             "hkv_last_error": ctypes.c_char_p, "hkv_local_kv_file_open": _vp,
+             "hkv_local_kv_file_close": None, "hkv_local_kv_file_write": _u64,
+             "hkv_local_kv_file_read": _u64}
 
 EXPORTED_SYMBOLS = tuple(_SIGS)
 
@@ -176,6 +187,45 @@ def _stream(s):
     if isinstance(s, int):
         return s
     return s.cuda_stream
+
+
+class BaseKVFile:
+    """Key-value file of save/load (include/types.h:291-330).  Subclasses
+    implement read and write over numpy arrays: read fills up to n records
+    and returns the count, write stores n records and returns the count."""
+
+    def read(self, n, dim, keys, values, scores):
+        raise NotImplementedError
+
+    def write(self, n, dim, keys, values, scores):
+        raise NotImplementedError
+
+
+class LocalKVFile(BaseKVFile):
+    """Three raw files: keys (u64), rows (dim values each), scores (u64)
+    (include/types.h:350-464); read and write run in the library."""
+
+    def __init__(self):
+        self._f = None
+
+    def open(self, keys_path, values_path, scores_path, mode):
+        self.close()
+        self._f = _LIB.hkv_local_kv_file_open(os.fsencode(keys_path), os.fsencode(values_path),
+                                              os.fsencode(scores_path), mode.encode())
+        return bool(self._f)
+
+    def close(self):
+        if self._f:
+            _LIB.hkv_local_kv_file_close(self._f)
+        self._f = None
+
+    def __del__(self):
+        if _LIB is not None:
+            self.close()
+
+
+_NP_VALUE = {0: "float32", 1: "float64", 2: "float16", 3: "uint16", 4: "int8", 5: "uint8",
+             6: "int16", 7: "uint16", 8: "int32", 9: "uint32", 10: "int64", 11: "uint64"}
 
 
 class HashTable:
@@ -295,6 +345,50 @@ class HashTable:
                                      _ptr(values), _ptr(scores),
                                      _stream(stream)))
         return int(cnt.item())
+
+    def _kv_callbacks(self, file):
+        if isinstance(file, LocalKVFile):
+            if not file._f:
+                raise HkvException("the key-value file is not open")
+            return (ctypes.cast(_LIB.hkv_local_kv_file_write, _KV_FN),
+                    ctypes.cast(_LIB.hkv_local_kv_file_read, _KV_FN), file._f)
+        import numpy as np
+        vt = np.dtype(_NP_VALUE[self.value_type])
+
+        def arrays(n, row_bytes, k, v, s):
+            dim = row_bytes // vt.itemsize
+            ka = np.ctypeslib.as_array(ctypes.cast(k, ctypes.POINTER(ctypes.c_uint64)), (n,))
+            va = np.ctypeslib.as_array(ctypes.cast(v, ctypes.POINTER(ctypes.c_uint8)),
+                                       (n * row_bytes,)).view(vt).reshape(n, dim)
+            sa = np.ctypeslib.as_array(ctypes.cast(s, ctypes.POINTER(ctypes.c_uint64)), (n,))
+            return dim, ka, va, sa
+
+        def w(ctx, n, row_bytes, k, v, s):
+            if n == 0:
+                return 0
+            dim, ka, va, sa = arrays(n, row_bytes, k, v, s)
+            return int(file.write(n, dim, ka, va, sa))
+
+        def r(ctx, n, row_bytes, k, v, s):
+            dim, ka, va, sa = arrays(n, row_bytes, k, v, s)
+            return int(file.read(n, dim, ka, va, sa))
+        return _KV_FN(w), _KV_FN(r), None
+
+    def save(self, file, max_workspace_size=1 << 20, stream=0):
+        """include/hkv_hashtable.h:3021-3118; returns the records written."""
+        w, _r, ctx = self._kv_callbacks(file)
+        out = _u64(0)
+        _check(_LIB.hkv_save(self._h, ctypes.cast(w, _vp), ctx, max_workspace_size,
+                             _stream(stream), ctypes.byref(out)))
+        return out.value
+
+    def load(self, file, max_workspace_size=1 << 20, stream=0):
+        """include/hkv_hashtable.h:3134-3195; returns the records read."""
+        _w, r, ctx = self._kv_callbacks(file)
+        out = _u64(0)
+        _check(_LIB.hkv_load(self._h, ctypes.cast(r, _vp), ctx, max_workspace_size,
+                             _stream(stream), ctypes.byref(out)))
+        return out.value
 
     def reserve(self, new_capacity, stream=0):
         _check(_LIB.hkv_reserve(self._h, new_capacity, _stream(stream)))

@@ -29,6 +29,8 @@
  *   HashTable::reserve          include/hkv_hashtable.h:2873-2935
  *   HashTable::load_factor      include/hkv_hashtable.h:2945-2947
  *   HashTable::set_global_epoch include/hkv_hashtable.h:3197
+ *   HashTable::save / load      include/hkv_hashtable.h:3021-3195
+ *   BaseKVFile / LocalKVFile    include/types.h:291-464
  *   capacity/dim/max_bucket_size/bucket_count/is_pure_hbm_mode accessors
  *                               include/hkv_hashtable.h:2849, :171-871
  * The launch glue it also replaces: include/aclnn_helper.h (reductions),
@@ -153,6 +155,46 @@ int hkv_export_batch(hkv_table* t, uint64_t n, uint64_t offset,
 
 /* Synchronous. */
 int hkv_reserve(hkv_table* t, uint64_t new_capacity, hkv_stream stream);
+/* Key-value files (include/types.h:291-464, BaseKVFile / LocalKVFile): a
+ * file is a pair of callbacks over `ctx`.  `row_bytes` = dim * sizeof(V);
+ * each returns the number of records read or written. */
+typedef uint64_t (*hkv_kv_write_fn)(void* ctx, uint64_t n, uint64_t row_bytes,
+                                    const void* keys, const void* values,
+                                    const uint64_t* scores);
+typedef uint64_t (*hkv_kv_read_fn)(void* ctx, uint64_t n, uint64_t row_bytes,
+                                   void* keys, void* values, uint64_t* scores);
+
+/* HashTable::save (include/hkv_hashtable.h:3021-3118): the live records in
+ * slot order, exported in chunks of max_workspace_size / (key + score + row)
+ * slots and handed to `write`; *count = records written.  Synchronizes
+ * `stream`.  Fails if max_workspace_size is below one record. */
+int hkv_save(hkv_table* t, hkv_kv_write_fn write, void* ctx,
+             uint64_t max_workspace_size, hkv_stream stream, uint64_t* count);
+
+/* HashTable::load (include/hkv_hashtable.h:3134-3195): chunks of
+ * max_workspace_size / (key + score + row) records read with `read`, each
+ * applied as insert_or_assign(unique_key = true, ignore_evict_strategy =
+ * true) after the global epoch is set to IGNORED (which it stays, as in the
+ * reference); *count = records read.  Synchronizes `stream`. */
+int hkv_load(hkv_table* t, hkv_kv_read_fn read, void* ctx,
+             uint64_t max_workspace_size, hkv_stream stream, uint64_t* count);
+
+/* LocalKVFile (include/types.h:350-464): three raw files (keys, rows,
+ * scores) opened with fopen `mode`; null if any fails to open.  Its read and
+ * write functions are the callbacks above, with the file as `ctx`; a read
+ * returns 0 when the three files do not yield the same count. */
+typedef struct hkv_local_kv_file hkv_local_kv_file;
+hkv_local_kv_file* hkv_local_kv_file_open(const char* keys_path,
+                                          const char* values_path,
+                                          const char* scores_path,
+                                          const char* mode);
+void hkv_local_kv_file_close(hkv_local_kv_file* f);
+uint64_t hkv_local_kv_file_write(void* f, uint64_t n, uint64_t row_bytes,
+                                 const void* keys, const void* values,
+                                 const uint64_t* scores);
+uint64_t hkv_local_kv_file_read(void* f, uint64_t n, uint64_t row_bytes,
+                                void* keys, void* values, uint64_t* scores);
+
 int hkv_set_global_epoch(hkv_table* t, uint64_t epoch);
 
 /* Synchronous (stream is synchronized). */

@@ -85,6 +85,50 @@ template <> struct value_code<uint64_t> { static constexpr int v = HKV_U64; };
 
 }  // namespace detail
 
+// Key-value files for save/load (include/types.h:291-464): the same
+// interface as the reference's BaseKVFile and LocalKVFile.
+template <class K, class V, class S>
+class BaseKVFile {
+ public:
+  virtual ~BaseKVFile() {}
+  // Reads up to n records into the buffers; returns the number read.
+  virtual size_t read(const size_t n, const size_t dim, K* keys, V* vectors, S* scores) = 0;
+  // Writes n records; returns the number written.
+  virtual size_t write(const size_t n, const size_t dim, const K* keys, const V* vectors,
+                       const S* scores) = 0;
+};
+
+// Three raw files (keys, vectors, scores) opened with fopen modes.
+template <class K, class V, class S>
+class LocalKVFile : public BaseKVFile<K, V, S> {
+ public:
+  LocalKVFile() {}
+  ~LocalKVFile() { close(); }
+  bool open(const std::string& keys_path, const std::string& values_path,
+            const std::string& scores_path, const char* mode) {
+    close();
+    f_ = hkv_local_kv_file_open(keys_path.c_str(), values_path.c_str(), scores_path.c_str(),
+                                mode);
+    return f_ != nullptr;
+  }
+  void close() noexcept {
+    hkv_local_kv_file_close(f_);
+    f_ = nullptr;
+  }
+  size_t read(const size_t n, const size_t dim, K* keys, V* vectors, S* scores) override {
+    return hkv_local_kv_file_read(f_, n, dim * sizeof(V), keys, vectors,
+                                  reinterpret_cast<uint64_t*>(scores));
+  }
+  size_t write(const size_t n, const size_t dim, const K* keys, const V* vectors,
+               const S* scores) override {
+    return hkv_local_kv_file_write(f_, n, dim * sizeof(V), keys, vectors,
+                                   reinterpret_cast<const uint64_t*>(scores));
+  }
+
+ private:
+  hkv_local_kv_file* f_ = nullptr;
+};
+
 template <typename K, typename V, typename S = uint64_t,
           int Strategy = EvictStrategy::kLru>
 class HashTable {
@@ -219,6 +263,25 @@ class HashTable {
 
   void set_global_epoch(uint64_t epoch) { detail::check(hkv_set_global_epoch(t_, epoch)); }
 
+  // include/hkv_hashtable.h:3021-3118: the live records in slot order,
+  // written to `file` in chunks of max_workspace_size / (key + score + row).
+  size_type save(BaseKVFile<K, V, S>* file, const size_t max_workspace_size = 1L * 1024 * 1024,
+                 aclrtStream stream = 0) const {
+    uint64_t n = 0;
+    detail::check(hkv_save(t_, &kv_write, file, max_workspace_size, stream, &n));
+    return n;
+  }
+
+  // include/hkv_hashtable.h:3134-3195: chunks read from `file`, each applied
+  // as insert_or_assign(unique_key = true, ignore_evict_strategy = true)
+  // with the global epoch set to IGNORED (as it stays afterwards).
+  size_type load(BaseKVFile<K, V, S>* file, const size_t max_workspace_size = 1L * 1024 * 1024,
+                 aclrtStream stream = 0) {
+    uint64_t n = 0;
+    detail::check(hkv_load(t_, &kv_read, file, max_workspace_size, stream, &n));
+    return n;
+  }
+
   size_type size(aclrtStream stream = 0) const {
     uint64_t s = 0;
     detail::check(hkv_size(t_, stream, &s));
@@ -253,6 +316,19 @@ class HashTable {
         hipStreamSynchronize(stream) != hipSuccess)
       throw NpuException("counter read failed");
     return h;
+  }
+
+  static uint64_t kv_write(void* ctx, uint64_t n, uint64_t row_bytes, const void* keys,
+                           const void* values, const uint64_t* scores) {
+    return static_cast<BaseKVFile<K, V, S>*>(ctx)->write(
+        n, row_bytes / sizeof(V), static_cast<const K*>(keys), static_cast<const V*>(values),
+        reinterpret_cast<const S*>(scores));
+  }
+  static uint64_t kv_read(void* ctx, uint64_t n, uint64_t row_bytes, void* keys, void* values,
+                          uint64_t* scores) {
+    return static_cast<BaseKVFile<K, V, S>*>(ctx)->read(
+        n, row_bytes / sizeof(V), static_cast<K*>(keys), static_cast<V*>(values),
+        reinterpret_cast<S*>(scores));
   }
 
   hkv_table* t_ = nullptr;
