@@ -14,7 +14,12 @@ enum ApplyOp {
   OP_INSERT_AND_EVICT = 2,
   OP_ACCUM_OR_ASSIGN = 3,
   OP_ASSIGN_SCORES = 4,
+  OP_FIND_OR_INSERT_PTR = 5,  // find_or_insert returning row addresses: no row moves
 };
+
+// Slot word of the pointer find_or_insert: global slot index + 1 (0 = no
+// slot), with this bit set when the key was found.
+constexpr uint64_t kSlotFound = 1ull << 63;
 
 // Eviction tie-break family: the reference's 16-lane digest kernels (unique
 // keys) or its 32-lane find_and_lock tiles (non-unique keys, accum_or_assign).
@@ -32,6 +37,9 @@ struct ApplyArgs {
   uint64_t* ev_counter;
   uint32_t* ev_bits;          // insert_and_evict: records at their batch index, flagged here
                               // (null: records appended at an atomic counter)
+  uint64_t* slot_out;         // pointer find_or_insert: slot word per batch index
+  int lock;                   // pointer find_or_insert: claimed and found slots hold
+                              // LOCKED until the batch ends
   uint64_t n;
   ScoreCtx sc;
   int rule;
@@ -92,6 +100,22 @@ void launch_apply(const TableView& t, int op, const ApplyArgs& a,
                   RouteScratch& rs, int parity, hipStream_t s);
 void launch_apply_part(const TableView& t, int op, const ApplyArgs& a,
                        const PartScratch& ps, hipStream_t s);
+// Pointer find_or_insert: placement in batch order, slot words in
+// ps.trow, then value / key addresses, founds, and (unless keep_locked) the
+// keys written back over LOCKED.
+void launch_find_or_insert_ptr(const TableView& t, const ApplyArgs& a, const PartScratch& ps,
+                               uint64_t* value_ptrs, uint8_t* founds, uint64_t* key_ptrs,
+                               bool keep_locked, hipStream_t s);
+// Row addresses of present keys; with `update`, the hit score functor runs
+// on each found key first (find_and_update).
+void launch_find_ptr(const TableView& t, const uint64_t* keys, uint64_t n,
+                     uint64_t* value_ptrs, uint8_t* founds, uint64_t* scores, bool update,
+                     const ScoreCtx& sc, hipStream_t s);
+void launch_lock_keys(const TableView& t, const uint64_t* keys, uint64_t n,
+                      uint64_t* key_ptrs, uint8_t* success, const uint64_t* scores,
+                      const ScoreCtx& sc, hipStream_t s);
+void launch_unlock_keys(const TableView& t, uint64_t n, const uint64_t* key_ptrs,
+                        const uint64_t* keys, uint8_t* success, hipStream_t s);
 void launch_export(const TableView& t, uint64_t offset, uint64_t n,
                    uint64_t* d_counter, uint64_t* keys, uint8_t* values,
                    uint64_t* scores, uint32_t* block_scratch, int unit,

@@ -576,7 +576,9 @@ __device__ __forceinline__ void apply_key_in(const TableView& t, Bucket16& S, co
         if (l == (start & 15u)) kk = rec_get(S.key, start >> 4);
         mk = shfl_u64(kk, (int)(start & 15u), 16);
       }
-      if (des < ms) {
+      if (des < ms || mk == kLockedKey) {
+        // A LOCKED victim is never taken: the reference kernels wait for it
+        // to be unlocked.
         res = R_REFUSED;
       } else {
         pos = mp;
@@ -617,7 +619,9 @@ __device__ __forceinline__ void apply_key_in(const TableView& t, Bucket16& S, co
   }
   if (res == R_EMPTY || res == R_RECLAIMED) S.bsz++;
 
-  if (res == R_DUP) {
+  if (OP == OP_FIND_OR_INSERT_PTR) {
+    // No row moves: the caller reads or writes the row through its address.
+  } else if (res == R_DUP) {
     if (OP == OP_FIND_OR_INSERT) {
       copy_units<U>(G(a.io_values) + i * (uint64_t)R, trow, R, l, 16);
     } else if (OP == OP_ACCUM_OR_ASSIGN) {
@@ -645,21 +649,32 @@ __device__ __forceinline__ void apply_key_in(const TableView& t, Bucket16& S, co
     } else {
       ns = score_new(a.sc, has_in, in, des, old, &w);
     }
+    // The pointer find_or_insert with unique keys holds every slot it claims
+    // or finds LOCKED for the rest of the batch (find_or_insert_ptr_kernel_v2.h:38-285):
+    // later keys neither match nor evict it.
+    const bool lk = OP == OP_FIND_OR_INSERT_PTR && a.lock;
+    const uint64_t wk = lk ? kLockedKey : k;
     if (res == R_DUP) {
       if (w) {
         slot_score(t, S.base + pos) = ns;
         rec_set(S.score, jj, ns);
       }
+      if (lk) {
+        slot_key(t, S.base + pos) = kLockedKey;
+        rec_set(S.key, jj, kLockedKey);
+      }
     } else if (w) {
-      slot_store(t, S.base + pos, k, ns);
+      slot_store(t, S.base + pos, wk, ns);
       G(t.digests)[S.base + pos] = (uint8_t)d;
       dg_set(S, jj, d);
-      rec_set(S.key, jj, k);
+      rec_set(S.key, jj, wk);
       rec_set(S.score, jj, ns);
     } else {
-      slot_key(t, S.base + pos) = k;
-      rec_set(S.key, jj, k);
+      slot_key(t, S.base + pos) = wk;
+      rec_set(S.key, jj, wk);
     }
+    if (OP == OP_FIND_OR_INSERT_PTR)
+      G(a.slot_out)[i] = (S.base + pos + 1) | (res == R_DUP ? kSlotFound : 0ull);
   }
 }
 
@@ -3239,6 +3254,219 @@ __global__ __launch_bounds__(kBlock) void k_apply_deferred(TableView t, ApplyArg
 }
 
 /* ------------------------------------------------------------------------ */
+/* pointer APIs: find*, find_and_update, find_or_insert*, lock / unlock      */
+/* ------------------------------------------------------------------------ */
+
+// Placement of the pointer find_or_insert: every partition, each bucket's
+// keys in batch order through apply_key, one 16-lane group per bucket.  A
+// partition's entries load in runs that end at a chunk boundary (one chunk's
+// entries of a partition are contiguous but unordered), so that a bucket's
+// keys in one run all precede its keys in the next.
+constexpr uint32_t kSeqCap = 2 * kPartChunk;  // entries per run
+
+template <int OP, int U>
+__global__ __launch_bounds__(kBlock) void k_apply_seq(TableView t, ApplyArgs a, PartScratch ps) {
+  __shared__ uint64_t s_key[kSeqCap];
+  __shared__ uint32_t s_idx[kSeqCap];
+  __shared__ uint8_t s_bk[kSeqCap];
+  __shared__ uint16_t s_ord[kSeqCap];  // run positions grouped by bucket
+  __shared__ uint16_t s_srt[kSeqCap];  // ... in batch order within each bucket
+  __shared__ uint32_t s_cnt[kPartBuckets], s_off[kPartBuckets], s_fill[kPartBuckets];
+  __shared__ uint32_t s_bl[kPartBuckets];  // buckets with keys in the run
+  __shared__ uint32_t s_w[kBlock / 64];
+  __shared__ uint32_t s_li, s_r1, s_nb;
+  const uint32_t tid = threadIdx.x, gl = tid & 15;
+  gptr<const u64x2> ent = G(reinterpret_cast<const u64x2*>(ps.ent));
+  for (;;) {
+    if (tid == 0) s_li = atomicAdd(&ps.dctr[3], 1u);
+    __syncthreads();
+    const uint32_t p = s_li;
+    if (p >= ps.np) break;  // block-uniform
+    const uint32_t base_e = ps.pinfo[2 * p], m = ps.pinfo[2 * p + 1];
+    const uint64_t part_b0 = (uint64_t)p * kPartBuckets;
+    for (uint32_t r0 = 0; r0 < m;) {
+      uint32_t r1 = m;
+      if (m - r0 > kSeqCap) {
+        // The chunk segment holding entry r0 + kSeqCap has at most
+        // kPartChunk entries, so it starts after r0 + kPartChunk.
+        const uint32_t cg = (uint32_t)(ent[base_e + r0 + kSeqCap].y / kPartChunk);
+        if (tid == 0) s_r1 = r0 + kSeqCap;
+        __syncthreads();
+        for (uint32_t x = r0 + kPartChunk + tid; x < r0 + kSeqCap; x += kBlock)
+          if ((uint32_t)(ent[base_e + x].y / kPartChunk) == cg) atomicMin(&s_r1, x);
+        __syncthreads();
+        r1 = s_r1;
+      }
+      const uint32_t mr = r1 - r0;
+      s_cnt[tid] = 0;
+      if (tid == 0) s_nb = 0;
+      __syncthreads();
+      for (uint32_t x = tid; x < mr; x += kBlock) {
+        const u64x2 e = ent[base_e + r0 + x];
+        const uint32_t bk = (uint32_t)(bucket_of(t, e.x) - part_b0);
+        s_key[x] = e.x;
+        s_idx[x] = (uint32_t)e.y;
+        s_bk[x] = (uint8_t)bk;
+        atomicAdd(&s_cnt[bk], 1u);
+      }
+      __syncthreads();
+      uint32_t tot;
+      const uint32_t c = s_cnt[tid];
+      const uint32_t off = block_excl_scan256(c, s_w, &tot);
+      s_off[tid] = off;
+      s_fill[tid] = off;
+      if (c) s_bl[atomicAdd(&s_nb, 1u)] = tid;
+      __syncthreads();
+      for (uint32_t x = tid; x < mr; x += kBlock)
+        s_ord[atomicAdd(&s_fill[s_bk[x]], 1u)] = (uint16_t)x;
+      __syncthreads();
+      const uint32_t nbk = s_nb;
+      for (uint32_t q = tid >> 4; q < nbk; q += kBlock / 16) {
+        const uint32_t bk = s_bl[q];
+        const uint32_t cc = s_cnt[bk], o = s_off[bk];
+        // Rank of each key by batch index (indices are distinct).
+        for (uint32_t x = gl; x < cc; x += 16) {
+          const uint32_t me = s_ord[o + x];
+          const uint32_t iv = s_idx[me];
+          uint32_t r = 0;
+          for (uint32_t y = 0; y < cc; y++) r += s_idx[s_ord[o + y]] < iv ? 1u : 0u;
+          s_srt[o + r] = (uint16_t)me;
+        }
+        group_sync();
+        Bucket16 S;
+        bucket_load(t, S, part_b0 + bk, gl);
+        for (uint32_t step = 0; step < cc; step++) {
+          const uint32_t x = s_srt[o + step];
+          apply_key<OP, U>(t, S, a, s_idx[x], s_key[x]);
+        }
+        bucket_finish(t, S);
+      }
+      __syncthreads();
+      r0 = r1;
+    }
+    __syncthreads();  // every thread has read s_li before it is rewritten
+  }
+}
+
+// Slot words -> value and key addresses and founds; with `restore`, the key
+// goes back over LOCKED (find_or_insert_ptr_kernel_unlock_key_vf,
+// find_or_insert_ptr_kernel_v2.h:287-303).  Clears the slot words.
+__global__ __launch_bounds__(kBlock) void k_ptr_finish(TableView t,
+                                                       const uint64_t* __restrict__ keys,
+                                                       uint64_t n, uint64_t* __restrict__ slot_w,
+                                                       uint64_t* __restrict__ vptrs,
+                                                       uint8_t* __restrict__ founds,
+                                                       uint64_t* __restrict__ kptrs, int restore) {
+  const uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (i >= n) return;
+  const uint64_t v = slot_w[i];
+  uint64_t vp = 0, kp = 0;
+  if (v) {
+    slot_w[i] = 0;
+    const uint64_t g = (v & ~kSlotFound) - 1;
+    vp = (uint64_t)(uintptr_t)row_ptr(t, g >> t.bshift, (uint32_t)(g & (t.B - 1)));
+    kp = (uint64_t)(uintptr_t)(t.slots + 2 * g);
+    if (restore) slot_key(t, g) = keys[i];
+  }
+  vptrs[i] = vp;
+  if (founds) founds[i] = (v & kSlotFound) ? 1 : 0;
+  if (kptrs) kptrs[i] = kp;
+}
+
+// find (pointer overload), find_ptr_with_digest_kernel.h:30-148, and
+// find_and_update (UPDATE), find_and_update_kernel_with_filter.h:35-165: the
+// row address of each present key, null otherwise; find_and_update first
+// applies the hit score functor and returns the score it leaves.
+template <bool UPDATE>
+__global__ __launch_bounds__(kBlock) void k_find_ptr(TableView t, const uint64_t* __restrict__ keys,
+                                                     uint64_t n, uint64_t* __restrict__ vptrs,
+                                                     uint8_t* __restrict__ founds,
+                                                     uint64_t* __restrict__ scores, ScoreCtx sc) {
+  const uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (i >= n) return;
+  const uint64_t k = keys[i];
+  int p = -1;
+  KeyPos q{};
+  if (!is_reserved(k)) {
+    q = key_pos(t, k);
+    p = probe_find(t, q.b, q.start, q.d, k, false);
+  }
+  if (p < 0) {
+    vptrs[i] = 0;
+    if (founds) founds[i] = 0;
+    return;
+  }
+  const uint64_t g = q.b * t.B + (uint32_t)p;
+  if (UPDATE) {
+    const bool has_in = scores != nullptr;
+    const uint64_t in = has_in ? scores[i] : 0;
+    const uint64_t old = slot_score(t, g);
+    bool w;
+    const uint64_t ns = score_hit(sc, has_in, in, score_desired(sc, has_in, in), old, &w);
+    if (w) slot_score(t, g) = ns;
+    if (scores) scores[i] = w ? ns : old;
+  } else if (scores) {
+    scores[i] = slot_score(t, g);
+  }
+  vptrs[i] = (uint64_t)(uintptr_t)row_ptr(t, q.b, (uint32_t)p);
+  if (founds) founds[i] = 1;
+}
+
+// lock_keys (lock_keys_kernel.h:31-141): a present key's slot goes from the
+// key to LOCKED with a CAS, so one occurrence of a repeated key wins; the
+// winner applies the hit score functor and returns the slot's key address.
+__global__ __launch_bounds__(kBlock) void k_lock_keys(TableView t, const uint64_t* __restrict__ keys,
+                                                      uint64_t n, uint64_t* __restrict__ kptrs,
+                                                      uint8_t* __restrict__ success,
+                                                      const uint64_t* __restrict__ scores,
+                                                      ScoreCtx sc) {
+  const uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (i >= n) return;
+  const uint64_t k = keys[i];
+  uint64_t kp = 0;
+  if (!is_reserved(k)) {
+    const KeyPos q = key_pos(t, k);
+    const int p = probe_find(t, q.b, q.start, q.d, k, false);
+    if (p >= 0) {
+      const uint64_t g = q.b * t.B + (uint32_t)p;
+      unsigned long long* ka = reinterpret_cast<unsigned long long*>(t.slots + 2 * g);
+      if (atomicCAS(ka, (unsigned long long)k, (unsigned long long)kLockedKey) ==
+          (unsigned long long)k) {
+        const bool has_in = scores != nullptr;
+        const uint64_t in = has_in ? scores[i] : 0;
+        bool w;
+        const uint64_t ns =
+            score_hit(sc, has_in, in, score_desired(sc, has_in, in), slot_score(t, g), &w);
+        if (w) slot_score(t, g) = ns;
+        kp = (uint64_t)(uintptr_t)ka;
+      }
+    }
+  }
+  kptrs[i] = kp;
+  if (success) success[i] = kp ? 1 : 0;
+}
+
+// unlock_keys (unlock_keys_kernel.h:40-79): LOCKED -> the caller's key.  An
+// address outside the table's key records, or a slot not holding LOCKED,
+// reports failure and writes nothing.
+__global__ __launch_bounds__(kBlock) void k_unlock_keys(TableView t, uint64_t n,
+                                                        const uint64_t* __restrict__ kptrs,
+                                                        const uint64_t* __restrict__ keys,
+                                                        uint8_t* __restrict__ success) {
+  const uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (i >= n) return;
+  const uint64_t p = kptrs[i];
+  const uint64_t lo = (uint64_t)(uintptr_t)t.slots, hi = lo + 16 * t.capacity;
+  bool ok = false;
+  if (p >= lo && p < hi && ((p - lo) & 15) == 0) {
+    unsigned long long* ka = reinterpret_cast<unsigned long long*>((uintptr_t)p);
+    ok = atomicCAS(ka, (unsigned long long)kLockedKey, (unsigned long long)keys[i]) ==
+         (unsigned long long)kLockedKey;
+  }
+  if (success) success[i] = ok ? 1 : 0;
+}
+
+/* ------------------------------------------------------------------------ */
 /* export_batch                                                              */
 /* ------------------------------------------------------------------------ */
 
@@ -3609,6 +3837,44 @@ void launch_apply_part(const TableView& t, int op, const ApplyArgs& a, const Par
     case OP_ACCUM_OR_ASSIGN: apply_part_op<OP_ACCUM_OR_ASSIGN>(t, a, ps, s); break;
     default: apply_part_op<OP_ASSIGN_SCORES>(t, a, ps, s); break;
   }
+}
+
+void launch_find_or_insert_ptr(const TableView& t, const ApplyArgs& a0, const PartScratch& ps,
+                               uint64_t* vptrs, uint8_t* founds, uint64_t* kptrs,
+                               bool keep_locked, hipStream_t s) {
+  ApplyArgs a = a0;
+  a.slot_out = ps.trow;
+  const size_t lds = (size_t)ps.np * sizeof(uint32_t);
+  hipLaunchKernelGGL(k_pcount, dim3(ps.chunks), dim3(kBlock), lds, s, t, a.keys, a.n, ps);
+  hipLaunchKernelGGL(k_pscan, dim3((ps.np + 15) / 16), dim3(1024), 0, s, ps);
+  hipLaunchKernelGGL(k_pscatter, dim3(ps.chunks), dim3(kBlock), lds, s, t, a.keys, a.n, ps);
+  const dim3 gp(ps.np < 2048 ? ps.np : 2048), b(kBlock);
+  hipLaunchKernelGGL((k_apply_seq<OP_FIND_OR_INSERT_PTR, 16>), gp, b, 0, s, t, a, ps);
+  hipLaunchKernelGGL(k_ptr_finish, dim3(grid_for(a.n, kBlock, 1ull << 31)), b, 0, s, t, a.keys,
+                     a.n, ps.trow, vptrs, founds, kptrs, (a.lock && !keep_locked) ? 1 : 0);
+}
+
+void launch_find_ptr(const TableView& t, const uint64_t* keys, uint64_t n, uint64_t* vptrs,
+                     uint8_t* founds, uint64_t* scores, bool update, const ScoreCtx& sc,
+                     hipStream_t s) {
+  const dim3 g(grid_for(n, kBlock, 1ull << 31)), b(kBlock);
+  if (update)
+    hipLaunchKernelGGL(k_find_ptr<true>, g, b, 0, s, t, keys, n, vptrs, founds, scores, sc);
+  else
+    hipLaunchKernelGGL(k_find_ptr<false>, g, b, 0, s, t, keys, n, vptrs, founds, scores, sc);
+}
+
+void launch_lock_keys(const TableView& t, const uint64_t* keys, uint64_t n, uint64_t* kptrs,
+                      uint8_t* success, const uint64_t* scores, const ScoreCtx& sc,
+                      hipStream_t s) {
+  hipLaunchKernelGGL(k_lock_keys, dim3(grid_for(n, kBlock, 1ull << 31)), dim3(kBlock), 0, s, t,
+                     keys, n, kptrs, success, scores, sc);
+}
+
+void launch_unlock_keys(const TableView& t, uint64_t n, const uint64_t* kptrs,
+                        const uint64_t* keys, uint8_t* success, hipStream_t s) {
+  hipLaunchKernelGGL(k_unlock_keys, dim3(grid_for(n, kBlock, 1ull << 31)), dim3(kBlock), 0, s, t,
+                     n, kptrs, keys, success);
 }
 
 void launch_export(const TableView& t, uint64_t offset, uint64_t n, uint64_t* d_counter,

@@ -977,6 +977,124 @@ int hkv_set_lru_clock(hkv_table* t, uint64_t clock, int enable) {
   });
 }
 
+int hkv_find_ptr(hkv_table* t, uint64_t n, const void* keys, void** value_ptrs,
+                 uint8_t* founds, uint64_t* scores, hkv_stream stream, int unique_key) {
+  return guarded([&] {
+    need_table(t);
+    // include/hkv_hashtable.h:2244-2262
+    (void)unique_key;
+    if (n == 0) return;
+    if (!keys || !value_ptrs) fail(HKV_ERR_INVALID, "keys and values must not be null");
+    launch_find_ptr(t->view(), reinterpret_cast<const uint64_t*>(keys), n,
+                    reinterpret_cast<uint64_t*>(value_ptrs), founds, scores, false, ScoreCtx{},
+                    S(stream));
+    hip_check(hipGetLastError(), "find launch");
+  });
+}
+
+int hkv_find_and_update(hkv_table* t, uint64_t n, const void* keys, void** value_ptrs,
+                        uint8_t* founds, uint64_t* scores, hkv_stream stream, int unique_key) {
+  return guarded([&] {
+    need_table(t);
+    // include/hkv_hashtable.h:2288-2317
+    if (n == 0) return;
+    if (!keys || !value_ptrs) fail(HKV_ERR_INVALID, "keys and values must not be null");
+    t->check_scores(t->strategy, scores, false);
+    if (!unique_key)
+      fail(HKV_ERR_RUNTIME,
+           "Not support update score when keys are not unique or bucket capacity is small.");
+    const ScoreCtx sc{t->strategy, t->epoch, t->clock_now()};
+    launch_find_ptr(t->view(), reinterpret_cast<const uint64_t*>(keys), n,
+                    reinterpret_cast<uint64_t*>(value_ptrs), founds, scores, true, sc,
+                    S(stream));
+    hip_check(hipGetLastError(), "find_and_update launch");
+  });
+}
+
+int hkv_find_or_insert_ptr(hkv_table* t, uint64_t n, const void* keys, void** value_ptrs,
+                           uint8_t* founds, const uint64_t* scores, hkv_stream stream,
+                           int unique_key, int ignore_evict_strategy, void** locked_key_ptrs) {
+  return guarded([&] {
+    need_table(t);
+    // include/hkv_hashtable.h:1658-1728
+    if (n == 0) return;
+    if (!keys || !value_ptrs || !founds)
+      fail(HKV_ERR_INVALID, "keys, values and founds must not be null");
+    const hipStream_t s = S(stream);
+    t->maybe_grow(n, s);
+    t->check_scores(t->strategy, scores, ignore_evict_strategy != 0);
+    if (locked_key_ptrs && !unique_key)
+      fail(HKV_ERR_UNSUPPORTED,
+           "unique_key should be true and max_bucket_size should be larger.");
+    PartScratch ps{};
+    if (!t->part_scratch(n, &ps, s))
+      fail(HKV_ERR_UNSUPPORTED,
+           "the pointer find_or_insert needs the partitioned apply path "
+           "(at most 2^29 slots, fewer than 2^32 keys per call)");
+    ApplyArgs a{};
+    a.keys = reinterpret_cast<const uint64_t*>(keys);
+    a.in_scores = scores;
+    a.n = n;
+    a.sc.strategy = t->strategy;
+    a.sc.epoch = t->epoch;
+    a.sc.clock = t->clock_now();
+    a.rule = unique_key ? RULE_DIGEST16 : RULE_TILE32;
+    a.lock = unique_key ? 1 : 0;
+    a.unit = 16;
+    a.value_type = t->value_type;
+    launch_find_or_insert_ptr(t->view(), a, ps, reinterpret_cast<uint64_t*>(value_ptrs), founds,
+                              reinterpret_cast<uint64_t*>(locked_key_ptrs),
+                              locked_key_ptrs != nullptr, s);
+    hip_check(hipGetLastError(), "find_or_insert launch");
+  });
+}
+
+int hkv_lock_keys(hkv_table* t, uint64_t n, const void* keys, void** locked_key_ptrs,
+                  uint8_t* success, hkv_stream stream, const uint64_t* scores) {
+  return guarded([&] {
+    need_table(t);
+    // include/hkv_hashtable.h:1744-1771
+    if (n == 0) return;
+    if (!keys || !locked_key_ptrs) fail(HKV_ERR_INVALID, "keys and locked_key_ptrs must not be null");
+    if ((t->strategy == HKV_EPOCH_LFU || t->strategy == HKV_CUSTOMIZED) && !scores)
+      fail(HKV_ERR_INVALID, "this evict strategy reads input scores; scores is null.");
+    const ScoreCtx sc{t->strategy, t->epoch, t->clock_now()};
+    launch_lock_keys(t->view(), reinterpret_cast<const uint64_t*>(keys), n,
+                     reinterpret_cast<uint64_t*>(locked_key_ptrs), success, scores, sc,
+                     S(stream));
+    hip_check(hipGetLastError(), "lock_keys launch");
+  });
+}
+
+int hkv_unlock_keys(hkv_table* t, uint64_t n, void* const* locked_key_ptrs, const void* keys,
+                    uint8_t* success, hkv_stream stream) {
+  return guarded([&] {
+    need_table(t);
+    // include/hkv_hashtable.h:1788-1804
+    if (n == 0) return;
+    if (!keys || !locked_key_ptrs) fail(HKV_ERR_INVALID, "keys and locked_key_ptrs must not be null");
+    launch_unlock_keys(t->view(), n, reinterpret_cast<const uint64_t*>(locked_key_ptrs),
+                       reinterpret_cast<const uint64_t*>(keys), success, S(stream));
+    hip_check(hipGetLastError(), "unlock_keys launch");
+  });
+}
+
+int hkv_slot_addresses(const hkv_table* t, uint64_t n, const uint64_t* slots, void** key_ptrs,
+                       void** value_ptrs) {
+  return guarded([&] {
+    need_table(t);
+    const uint64_t mask = (1ull << t->slice_shift) - 1;
+    for (uint64_t i = 0; i < n; i++) {
+      const uint64_t g = slots[i];
+      if (g >= t->C) fail(HKV_ERR_INVALID, "slot index out of range");
+      const uint64_t b = g / t->B, sl = g % t->B;
+      if (key_ptrs) key_ptrs[i] = t->slots + 2 * g;
+      if (value_ptrs)
+        value_ptrs[i] = t->slices[b >> t->slice_shift].dev_ptr + ((b & mask) * t->B + sl) * t->row;
+    }
+  });
+}
+
 int hkv_live_count(hkv_table* t, hkv_stream stream, uint64_t* out) {
   return guarded([&] {
     need_table(t);

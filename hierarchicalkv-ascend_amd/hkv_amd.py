@@ -102,6 +102,13 @@ _SIGS = {
     "hkv_assign_scores": [_vp, _u64, _vp, _vp, _vp, _i32],
     "hkv_find": [_vp, _u64, _vp, _vp, _vp, _vp, _vp],
     "hkv_find_missed": [_vp, _u64, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
+    "hkv_find_ptr": [_vp, _u64, _vp, _vp, _vp, _vp, _vp, _i32],
+    "hkv_find_and_update": [_vp, _u64, _vp, _vp, _vp, _vp, _vp, _i32],
+    "hkv_find_or_insert_ptr": [_vp, _u64, _vp, _vp, _vp, _vp, _vp, _i32, _i32,
+                               _vp],
+    "hkv_lock_keys": [_vp, _u64, _vp, _vp, _vp, _vp, _vp],
+    "hkv_unlock_keys": [_vp, _u64, _vp, _vp, _vp, _vp],
+    "hkv_slot_addresses": [_vp, _u64, _vp, _vp, _vp],
     "hkv_erase": [_vp, _u64, _vp, _vp],
     "hkv_clear": [_vp, _vp],
     "hkv_export_batch": [_vp, _u64, _u64, _vp, _vp, _vp, _vp, _vp],
@@ -322,6 +329,56 @@ class HashTable:
                                     _ptr(missed_keys), _ptr(missed_indices),
                                     _ptr(missed_size), _ptr(scores),
                                     _stream(stream)))
+
+    # --- pointer APIs --------------------------------------------------------
+    # The reference overloads find / find_or_insert on `V**`; here the
+    # pointer forms have their own names.  Address arrays are uint64/int64
+    # tensors of n entries (0 = null).
+    def find_ptr(self, n, keys, values, founds=None, scores=None, stream=0,
+                 unique_key=True):
+        """find, pointer overload (include/hkv_hashtable.h:2244-2262)."""
+        _check(_LIB.hkv_find_ptr(self._h, n, _ptr(keys), _ptr(values),
+                                 _ptr(founds), _ptr(scores), _stream(stream),
+                                 int(unique_key)))
+
+    def find_and_update(self, n, keys, values, founds=None, scores=None,
+                        stream=0, unique_key=True):
+        """include/hkv_hashtable.h:2288-2317; scores are input and output."""
+        _check(_LIB.hkv_find_and_update(self._h, n, _ptr(keys), _ptr(values),
+                                        _ptr(founds), _ptr(scores),
+                                        _stream(stream), int(unique_key)))
+
+    def find_or_insert_ptr(self, n, keys, values, founds, scores=None, stream=0,
+                           unique_key=True, ignore_evict_strategy=False,
+                           locked_key_ptrs=None):
+        """find_or_insert, pointer overload (include/hkv_hashtable.h:1658-1728)."""
+        _check(_LIB.hkv_find_or_insert_ptr(self._h, n, _ptr(keys), _ptr(values),
+                                           _ptr(founds), _ptr(scores),
+                                           _stream(stream), int(unique_key),
+                                           int(ignore_evict_strategy),
+                                           _ptr(locked_key_ptrs)))
+
+    def lock_keys(self, n, keys, locked_key_ptrs, success=None, stream=0,
+                  scores=None):
+        """include/hkv_hashtable.h:1744-1771."""
+        _check(_LIB.hkv_lock_keys(self._h, n, _ptr(keys), _ptr(locked_key_ptrs),
+                                  _ptr(success), _stream(stream), _ptr(scores)))
+
+    def unlock_keys(self, n, locked_key_ptrs, keys, success=None, stream=0):
+        """include/hkv_hashtable.h:1788-1804."""
+        _check(_LIB.hkv_unlock_keys(self._h, n, _ptr(locked_key_ptrs),
+                                    _ptr(keys), _ptr(success), _stream(stream)))
+
+    def slot_addresses(self, slots):
+        """Test hook: (key word, value row) addresses of global slots, as
+        numpy uint64 arrays (no device work)."""
+        import numpy as np
+        sl = np.ascontiguousarray(slots, dtype=np.uint64)
+        kp = np.zeros(sl.size, np.uint64)
+        vp = np.zeros(sl.size, np.uint64)
+        _check(_LIB.hkv_slot_addresses(self._h, sl.size, sl.ctypes.data,
+                                       kp.ctypes.data, vp.ctypes.data))
+        return kp, vp
 
     # --- maintenance ---------------------------------------------------------
     def erase(self, n, keys, stream=0):

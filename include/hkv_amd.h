@@ -19,9 +19,15 @@
  *   HashTable::insert_and_evict include/hkv_hashtable.h:1260-1324, :1368-1396
  *   HashTable::accum_or_assign  include/hkv_hashtable.h:1438-1507
  *   HashTable::find_or_insert   include/hkv_hashtable.h:1526-1632
+ *   HashTable::find_or_insert (value and key pointers)
+ *                               include/hkv_hashtable.h:1658-1728
+ *   HashTable::lock_keys        include/hkv_hashtable.h:1744-1771
+ *   HashTable::unlock_keys      include/hkv_hashtable.h:1788-1804
  *   HashTable::assign_scores    include/hkv_hashtable.h:1943-1977
  *   HashTable::find             include/hkv_hashtable.h:2113-2152
  *   HashTable::find (missed)    include/hkv_hashtable.h:2175-2220
+ *   HashTable::find (pointers)  include/hkv_hashtable.h:2244-2262
+ *   HashTable::find_and_update  include/hkv_hashtable.h:2288-2317
  *   HashTable::erase            include/hkv_hashtable.h:2358-2376
  *   HashTable::clear            include/hkv_hashtable.h:2482-2493
  *   HashTable::export_batch     include/hkv_hashtable.h:2519-2577
@@ -54,7 +60,8 @@ enum hkv_status {
   HKV_OK = 0,
   HKV_ERR_INVALID = 1,     /* argument/option check (HkvException)        */
   HKV_ERR_RUNTIME = 2,     /* unsupported mode for this call (runtime_error) */
-  HKV_ERR_UNSUPPORTED = 3, /* not available in this build                 */
+  HKV_ERR_UNSUPPORTED = 3, /* option or argument combination not accepted
+                              (std::invalid_argument)                    */
   HKV_ERR_DEVICE = 4,      /* HIP runtime failure (NpuException)          */
 };
 
@@ -144,6 +151,52 @@ int hkv_find_missed(hkv_table* t, uint64_t n, const void* keys, void* values,
                     void* missed_keys, int32_t* missed_indices,
                     int32_t* missed_size, uint64_t* scores, hkv_stream stream);
 
+/* Pointer APIs.  `value_ptrs[i]` receives the address of key i's value row
+ * (device-accessible: HBM, or pinned host memory in hybrid mode) or NULL;
+ * `key_ptrs` entries are addresses of the table's key words.  Addresses stay
+ * valid until the table grows (reserve or automatic growth) or is cleared.
+ *
+ * find: rows of present keys; `founds` and `scores` may be NULL, scores are
+ * written for found keys only.  unique_key is accepted as in the reference. */
+int hkv_find_ptr(hkv_table* t, uint64_t n, const void* keys, void** value_ptrs,
+                 uint8_t* founds, uint64_t* scores, hkv_stream stream,
+                 int unique_key);
+
+/* find_and_update: find, then the hit score functor on each found key
+ * (scores are input and output, as in the reference).  unique_key must be
+ * 1 (runtime_error otherwise); scores follow the strategy checks. */
+int hkv_find_and_update(hkv_table* t, uint64_t n, const void* keys,
+                        void** value_ptrs, uint8_t* founds, uint64_t* scores,
+                        hkv_stream stream, int unique_key);
+
+/* find_or_insert, pointer overload: places keys exactly like
+ * hkv_find_or_insert but moves no rows; a new key's row keeps whatever the
+ * slot held, for the caller to write.  `founds` is required.  With
+ * unique_key, every slot the batch claims or finds stays LOCKED until the
+ * batch ends, so later keys of the batch cannot evict it; with
+ * `locked_key_ptrs` non-NULL (unique_key required, invalid_argument
+ * otherwise) the keys stay LOCKED after the call and their key addresses
+ * are returned for hkv_unlock_keys.  Refused and reserved keys get NULL
+ * addresses and founds 0. */
+int hkv_find_or_insert_ptr(hkv_table* t, uint64_t n, const void* keys,
+                           void** value_ptrs, uint8_t* founds,
+                           const uint64_t* scores, hkv_stream stream,
+                           int unique_key, int ignore_evict_strategy,
+                           void** locked_key_ptrs);
+
+/* lock_keys: a present key's slot key becomes LOCKED (found by find* no
+ * more, never evicted) and the hit score functor runs with `scores` (may be
+ * NULL except for EpochLfu and Customized).  `success` may be NULL. */
+int hkv_lock_keys(hkv_table* t, uint64_t n, const void* keys,
+                  void** locked_key_ptrs, uint8_t* success, hkv_stream stream,
+                  const uint64_t* scores);
+
+/* unlock_keys: LOCKED -> keys[i] at each address.  An address that is not
+ * one of this table's key words, or whose word is not LOCKED, reports 0 in
+ * `success` (may be NULL) and is not written. */
+int hkv_unlock_keys(hkv_table* t, uint64_t n, void* const* locked_key_ptrs,
+                    const void* keys, uint8_t* success, hkv_stream stream);
+
 int hkv_erase(hkv_table* t, uint64_t n, const void* keys, hkv_stream stream);
 int hkv_clear(hkv_table* t, hkv_stream stream);
 
@@ -218,6 +271,12 @@ int hkv_set_lru_clock(hkv_table* t, uint64_t clock, int enable);
  * maintain on the device (it selects the find probe order).  Synchronizes
  * `stream`; equals hkv_size() after every completed call. */
 int hkv_live_count(hkv_table* t, hkv_stream stream, uint64_t* out);
+
+/* Test hook with no reference counterpart: host-side addresses of the key
+ * word and value row of global slots (bucket * max_bucket_size + slot), for
+ * checking returned pointers against a slot layout.  No device work. */
+int hkv_slot_addresses(const hkv_table* t, uint64_t n, const uint64_t* slots,
+                       void** key_ptrs, void** value_ptrs);
 
 #ifdef __cplusplus
 }

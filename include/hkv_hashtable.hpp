@@ -219,6 +219,31 @@ class HashTable {
                                      ignore_evict_strategy));
   }
 
+  // Pointer overload: value-row addresses instead of row copies; with
+  // locked_key_ptrs the keys stay LOCKED for unlock_keys.
+  void find_or_insert(size_type n, const key_type* keys, value_type** values, bool* founds,
+                      score_type* scores = nullptr, aclrtStream stream = 0,
+                      bool unique_key = true, bool ignore_evict_strategy = false,
+                      key_type** locked_key_ptrs = nullptr) {
+    detail::check(hkv_find_or_insert_ptr(
+        t_, n, keys, reinterpret_cast<void**>(values), reinterpret_cast<uint8_t*>(founds),
+        scores, stream, unique_key, ignore_evict_strategy,
+        reinterpret_cast<void**>(locked_key_ptrs)));
+  }
+
+  void lock_keys(size_type n, const key_type* keys, key_type** locked_key_ptrs,
+                 bool* success = nullptr, aclrtStream stream = 0,
+                 const score_type* scores = nullptr) {
+    detail::check(hkv_lock_keys(t_, n, keys, reinterpret_cast<void**>(locked_key_ptrs),
+                                reinterpret_cast<uint8_t*>(success), stream, scores));
+  }
+
+  void unlock_keys(size_type n, key_type** locked_key_ptrs, const key_type* keys,
+                   bool* success = nullptr, aclrtStream stream = 0) {
+    detail::check(hkv_unlock_keys(t_, n, reinterpret_cast<void* const*>(locked_key_ptrs), keys,
+                                  reinterpret_cast<uint8_t*>(success), stream));
+  }
+
   void assign_scores(size_type n, const key_type* keys, const score_type* scores = nullptr,
                      aclrtStream stream = 0, bool unique_key = true) {
     detail::check(hkv_assign_scores(t_, n, keys, scores, stream, unique_key));
@@ -235,6 +260,21 @@ class HashTable {
             aclrtStream stream = 0) const {
     detail::check(hkv_find_missed(t_, n, keys, values, missed_keys, missed_indices,
                                   missed_size, scores, stream));
+  }
+
+  // Pointer overload of find: value-row addresses (null when missing).
+  void find(size_type n, const key_type* keys, value_type** values, bool* founds,
+            score_type* scores = nullptr, aclrtStream stream = 0, bool unique_key = true) const {
+    detail::check(hkv_find_ptr(t_, n, keys, reinterpret_cast<void**>(values),
+                               reinterpret_cast<uint8_t*>(founds), scores, stream, unique_key));
+  }
+
+  void find_and_update(size_type n, const key_type* keys, value_type** values, bool* founds,
+                       score_type* scores = nullptr, aclrtStream stream = 0,
+                       bool unique_key = true) {
+    detail::check(hkv_find_and_update(t_, n, keys, reinterpret_cast<void**>(values),
+                                      reinterpret_cast<uint8_t*>(founds), scores, stream,
+                                      unique_key));
   }
 
   void erase(size_type n, const key_type* keys, aclrtStream stream = 0) {

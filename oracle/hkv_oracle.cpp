@@ -171,7 +171,11 @@ struct Loc {
 // accum_or_assign).
 enum Rule { RULE_DIGEST16 = 0, RULE_TILE32 = 1 };
 
-enum Op { OP_INSERT_OR_ASSIGN, OP_FIND_OR_INSERT, OP_INSERT_AND_EVICT, OP_ACCUM };
+enum Op {
+  OP_INSERT_OR_ASSIGN, OP_FIND_OR_INSERT, OP_INSERT_AND_EVICT, OP_ACCUM,
+  OP_FIND_OR_INSERT_PTR,  // pointer overload: slots recorded, no row moves
+};
+constexpr uint64_t SLOT_FOUND = 1ull << 63;
 
 struct Record {
   uint64_t idx;
@@ -190,6 +194,12 @@ struct hkvo_table {
   bool reach_max = false;
   uint64_t epoch = IGNORED_EPOCH;
   int threads = 1;
+  // Pointer find_or_insert: slot word per batch index (global slot + 1, with
+  // SLOT_FOUND), and whether claimed / found slots stay LOCKED for the rest
+  // of the batch (the unique-key kernel holds its locks until the batch ends,
+  // find_or_insert_ptr_kernel_v2.h:38-303).
+  uint64_t* slot_out = nullptr;
+  bool lock_batch = false;
   uint8_t empty_d = 0, reclaim_d = 0;
   size_t row = 0;
   std::vector<uint8_t> dg;
@@ -462,6 +472,9 @@ struct hkvo_table {
     locate_key(k, &b, &start, &d);
     Loc L = locate(b, start, d, k, i, des, rule);
     const uint64_t base = b * B;
+    // A LOCKED victim is never taken: the reference kernels wait for it to
+    // be unlocked (insert_or_assign_kernel.h:240-268, find_utils.h:160-224).
+    if (L.res == R_EVICT && L.victim_key == LOCKED_KEY) L.res = R_REFUSED;
 
     if (op == OP_ACCUM) {
       if (L.res == R_REFUSED) return;
@@ -490,7 +503,9 @@ struct hkvo_table {
       recs->push_back(std::move(r));
     }
     // Row movement.
-    if (op == OP_FIND_OR_INSERT && L.res == R_DUP) {
+    if (op == OP_FIND_OR_INSERT_PTR) {
+      // none: the caller goes through the returned row address
+    } else if (op == OP_FIND_OR_INSERT && L.res == R_DUP) {
       std::memcpy(io_vals + i * row, rowp(b, p), row);
     } else if (op == OP_ACCUM && L.res == R_DUP) {
       accum_row(rowp(b, p), in_vals + i * row);
@@ -512,7 +527,9 @@ struct hkvo_table {
         dg[base + p] = d;
       }
     }
-    keys[base + p] = k;
+    keys[base + p] = (op == OP_FIND_OR_INSERT_PTR && lock_batch) ? LOCKED_KEY : k;
+    if (op == OP_FIND_OR_INSERT_PTR)
+      slot_out[i] = (base + p + 1) | (L.res == R_DUP ? SLOT_FOUND : 0);
   }
 
   /* ---- rehash, include/kernels/rehash_kernel/rehash_kernel.h:29-207 ------- */
@@ -850,6 +867,146 @@ int hkvo_find(hkvo_table* t, uint64_t n, const uint64_t* keys, void* values,
       }
     }
     if (founds) founds[i] = found ? 1 : 0;
+  }
+  return HKVO_OK;
+}
+
+int hkvo_find_ptr(hkvo_table* t, uint64_t n, const uint64_t* keys,
+                  uint64_t* slots, uint8_t* founds, uint64_t* scores) {
+  // include/kernels/find_ptr_kernel/find_ptr_with_digest_kernel.h:30-148
+  for (uint64_t i = 0; i < n; i++) {
+    const uint64_t k = keys[i];
+    slots[i] = HKVO_NO_SLOT;
+    if (founds) founds[i] = 0;
+    if (is_reserved(k)) continue;
+    uint64_t b;
+    uint32_t s;
+    uint8_t d;
+    t->locate_key(k, &b, &s, &d);
+    const int64_t p = t->find_slot(b, s, d, k);
+    if (p < 0) continue;
+    slots[i] = b * t->B + (uint64_t)p;
+    if (founds) founds[i] = 1;
+    if (scores) scores[i] = t->scores[slots[i]];
+  }
+  return HKVO_OK;
+}
+
+int hkvo_find_and_update(hkvo_table* t, uint64_t n, const uint64_t* keys,
+                         uint64_t* slots, uint8_t* founds, uint64_t* scores,
+                         int unique_key, uint64_t clock) {
+  // include/hkv_hashtable.h:2288-2317 and
+  // include/kernels/find_and_update_kernel/find_and_update_kernel_with_filter.h:35-165:
+  // a found key takes update_score_only(new_insert=false) with
+  // desired_when_missed, and its score after the update is returned.
+  if (n == 0) return HKVO_OK;
+  int rc = t->check(t->strategy, scores, false);
+  if (rc) return rc;
+  if (!unique_key) return HKVO_ERR_RUNTIME;
+  const bool has_in = scores != nullptr;
+  for (uint64_t i = 0; i < n; i++) {
+    const uint64_t k = keys[i];
+    slots[i] = HKVO_NO_SLOT;
+    if (founds) founds[i] = 0;
+    if (is_reserved(k)) continue;
+    uint64_t b;
+    uint32_t s;
+    uint8_t d;
+    t->locate_key(k, &b, &s, &d);
+    const int64_t p = t->find_slot(b, s, d, k);
+    if (p < 0) continue;
+    const uint64_t g = b * t->B + (uint64_t)p;
+    const uint64_t in = has_in ? scores[i] : 0;
+    const uint64_t des = desired(t->strategy, has_in, in, t->epoch, clock);
+    bool w;
+    const uint64_t ns = score_hit(t->strategy, has_in, in, des, t->scores[g], &w);
+    if (w) t->scores[g] = ns;
+    slots[i] = g;
+    if (founds) founds[i] = 1;
+    if (scores) scores[i] = t->scores[g];
+  }
+  return HKVO_OK;
+}
+
+int hkvo_find_or_insert_ptr(hkvo_table* t, uint64_t n, const uint64_t* keys,
+                            uint64_t* slots, uint8_t* founds,
+                            const uint64_t* scores, int unique_key, int ignore,
+                            int keep_locked, uint64_t clock) {
+  // include/hkv_hashtable.h:1658-1728.  unique_key: the lock-key kernel
+  // (digest-16 probe and eviction, find_or_insert_ptr_kernel_v2.h:38-285)
+  // holds each claimed or found slot LOCKED until the batch ends, then the
+  // unlock kernel (:287-303) writes the keys back unless the caller keeps
+  // them locked.  Otherwise find_or_insert_ptr_kernel_vf_v2 (:305-386):
+  // find_and_lock tiles, each key unlocked right after its own step.
+  if (n == 0) return HKVO_OK;
+  t->maybe_grow(n);
+  int rc = t->check(t->strategy, scores, ignore != 0);
+  if (rc) return rc;
+  if (keep_locked && !unique_key) return HKVO_ERR_UNSUPPORTED;
+  std::vector<uint64_t> w(n, 0);
+  t->slot_out = w.data();
+  t->lock_batch = unique_key != 0;
+  t->upsert_batch(OP_FIND_OR_INSERT_PTR, unique_key ? RULE_DIGEST16 : RULE_TILE32,
+                  t->strategy, n, keys, nullptr, nullptr, scores, nullptr, clock,
+                  nullptr);
+  t->slot_out = nullptr;
+  t->lock_batch = false;
+  for (uint64_t i = 0; i < n; i++) {
+    if (w[i] == 0) {
+      slots[i] = HKVO_NO_SLOT;
+      founds[i] = 0;
+      continue;
+    }
+    slots[i] = (w[i] & ~SLOT_FOUND) - 1;
+    founds[i] = (w[i] & SLOT_FOUND) ? 1 : 0;
+    if (unique_key && !keep_locked) t->keys[slots[i]] = keys[i];
+  }
+  return HKVO_OK;
+}
+
+int hkvo_lock_keys(hkvo_table* t, uint64_t n, const uint64_t* keys,
+                   uint64_t* slots, uint8_t* success, const uint64_t* scores,
+                   uint64_t clock) {
+  // include/kernels/lock_keys_kernel/lock_keys_kernel.h:31-141, keys in batch
+  // order: a present key's slot becomes LOCKED and takes
+  // update_with_digest(new_insert=false); a repeated key is no longer
+  // present for its later occurrences.
+  if (n == 0) return HKVO_OK;
+  const int st = t->strategy;
+  if ((st == kEpochLfu || st == kCustomized) && !scores) return HKVO_ERR_INVALID;
+  const bool has_in = scores != nullptr;
+  for (uint64_t i = 0; i < n; i++) {
+    const uint64_t k = keys[i];
+    slots[i] = HKVO_NO_SLOT;
+    if (success) success[i] = 0;
+    if (is_reserved(k)) continue;
+    uint64_t b;
+    uint32_t s;
+    uint8_t d;
+    t->locate_key(k, &b, &s, &d);
+    const int64_t p = t->find_slot(b, s, d, k);
+    if (p < 0) continue;
+    const uint64_t g = b * t->B + (uint64_t)p;
+    t->keys[g] = LOCKED_KEY;
+    const uint64_t in = has_in ? scores[i] : 0;
+    bool w;
+    const uint64_t ns = score_hit(st, has_in, in, desired(st, has_in, in, t->epoch, clock),
+                                  t->scores[g], &w);
+    if (w) t->scores[g] = ns;
+    slots[i] = g;
+    if (success) success[i] = 1;
+  }
+  return HKVO_OK;
+}
+
+int hkvo_unlock_keys(hkvo_table* t, uint64_t n, const uint64_t* slots,
+                     const uint64_t* keys, uint8_t* success) {
+  // include/kernels/unlock_keys_kernel/unlock_keys_kernel.h:40-79
+  for (uint64_t i = 0; i < n; i++) {
+    const uint64_t g = slots[i];
+    const bool ok = g < t->C && t->keys[g] == LOCKED_KEY;
+    if (ok) t->keys[g] = keys[i];
+    if (success) success[i] = ok ? 1 : 0;
   }
   return HKVO_OK;
 }

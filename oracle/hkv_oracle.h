@@ -68,6 +68,23 @@ int hkvo_accum_or_assign(hkvo_table* t, uint64_t n, const uint64_t* keys,
                          uint64_t clock);
 int hkvo_assign_scores(hkvo_table* t, uint64_t n, const uint64_t* keys,
                        const uint64_t* scores, uint64_t clock);
+/* Pointer APIs: slot indices (bucket * B + slot) stand for the addresses the
+ * product returns; HKVO_NO_SLOT for none. */
+#define HKVO_NO_SLOT 0xFFFFFFFFFFFFFFFFull
+int hkvo_find_ptr(hkvo_table* t, uint64_t n, const uint64_t* keys,
+                  uint64_t* slots, uint8_t* founds, uint64_t* scores);
+int hkvo_find_and_update(hkvo_table* t, uint64_t n, const uint64_t* keys,
+                         uint64_t* slots, uint8_t* founds, uint64_t* scores,
+                         int unique_key, uint64_t clock);
+int hkvo_find_or_insert_ptr(hkvo_table* t, uint64_t n, const uint64_t* keys,
+                            uint64_t* slots, uint8_t* founds,
+                            const uint64_t* scores, int unique_key, int ignore,
+                            int keep_locked, uint64_t clock);
+int hkvo_lock_keys(hkvo_table* t, uint64_t n, const uint64_t* keys,
+                   uint64_t* slots, uint8_t* success, const uint64_t* scores,
+                   uint64_t clock);
+int hkvo_unlock_keys(hkvo_table* t, uint64_t n, const uint64_t* slots,
+                     const uint64_t* keys, uint8_t* success);
 int hkvo_erase(hkvo_table* t, uint64_t n, const uint64_t* keys);
 void hkvo_clear(hkvo_table* t);
 uint64_t hkvo_export_batch(hkvo_table* t, uint64_t n, uint64_t offset,

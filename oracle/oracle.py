@@ -94,8 +94,20 @@ def lib():
                                                 ctypes.c_uint64,
                                                 ctypes.c_uint64,
                                                 ctypes.c_uint64]
+        L.hkvo_find_ptr.argtypes = [vp, ctypes.c_uint64, vp, vp, vp, vp]
+        L.hkvo_find_and_update.argtypes = [vp, ctypes.c_uint64, vp, vp, vp, vp,
+                                           ctypes.c_int, ctypes.c_uint64]
+        L.hkvo_find_or_insert_ptr.argtypes = [vp, ctypes.c_uint64, vp, vp, vp,
+                                              vp, ctypes.c_int, ctypes.c_int,
+                                              ctypes.c_int, ctypes.c_uint64]
+        L.hkvo_lock_keys.argtypes = [vp, ctypes.c_uint64, vp, vp, vp, vp,
+                                     ctypes.c_uint64]
+        L.hkvo_unlock_keys.argtypes = [vp, ctypes.c_uint64, vp, vp, vp]
         _LIB = L
     return _LIB
+
+
+NO_SLOT = 0xFFFFFFFFFFFFFFFF
 
 
 def _p(a):
@@ -227,6 +239,61 @@ class Oracle:
         s = None if scores is None else np.ascontiguousarray(scores, np.uint64)
         _chk(lib().hkvo_assign_scores(self.h, keys.size, _p(keys), _p(s),
                                       clock))
+
+    # --- pointer APIs: global slot indices (NO_SLOT for none) ----------------
+    def find_ptr(self, keys, with_scores=False):
+        keys = np.ascontiguousarray(keys, dtype=np.uint64)
+        n = keys.size
+        slots = np.zeros(n, np.uint64)
+        founds = np.zeros(n, np.uint8)
+        scores = np.zeros(n, np.uint64) if with_scores else None
+        _chk(lib().hkvo_find_ptr(self.h, n, _p(keys), _p(slots), _p(founds),
+                                 _p(scores)))
+        return slots, founds.astype(bool), scores
+
+    def find_and_update(self, keys, scores=None, unique_key=True, clock=0):
+        """Returns (slots, founds, scores after the call)."""
+        keys = np.ascontiguousarray(keys, dtype=np.uint64)
+        n = keys.size
+        slots = np.zeros(n, np.uint64)
+        founds = np.zeros(n, np.uint8)
+        s = None if scores is None else np.array(scores, np.uint64)
+        _chk(lib().hkvo_find_and_update(self.h, n, _p(keys), _p(slots),
+                                        _p(founds), _p(s), int(unique_key),
+                                        clock))
+        return slots, founds.astype(bool), s
+
+    def find_or_insert_ptr(self, keys, scores=None, unique_key=True,
+                           ignore_evict_strategy=False, keep_locked=False,
+                           clock=0):
+        keys = np.ascontiguousarray(keys, dtype=np.uint64)
+        n = keys.size
+        slots = np.zeros(n, np.uint64)
+        founds = np.zeros(n, np.uint8)
+        s = None if scores is None else np.ascontiguousarray(scores, np.uint64)
+        _chk(lib().hkvo_find_or_insert_ptr(self.h, n, _p(keys), _p(slots),
+                                           _p(founds), _p(s), int(unique_key),
+                                           int(ignore_evict_strategy),
+                                           int(keep_locked), clock))
+        return slots, founds.astype(bool)
+
+    def lock_keys(self, keys, scores=None, clock=0):
+        keys = np.ascontiguousarray(keys, dtype=np.uint64)
+        n = keys.size
+        slots = np.zeros(n, np.uint64)
+        ok = np.zeros(n, np.uint8)
+        s = None if scores is None else np.ascontiguousarray(scores, np.uint64)
+        _chk(lib().hkvo_lock_keys(self.h, n, _p(keys), _p(slots), _p(ok), _p(s),
+                                  clock))
+        return slots, ok.astype(bool)
+
+    def unlock_keys(self, slots, keys):
+        slots = np.ascontiguousarray(slots, dtype=np.uint64)
+        keys = np.ascontiguousarray(keys, dtype=np.uint64)
+        ok = np.zeros(keys.size, np.uint8)
+        _chk(lib().hkvo_unlock_keys(self.h, keys.size, _p(slots), _p(keys),
+                                    _p(ok)))
+        return ok.astype(bool)
 
     def erase(self, keys):
         keys = np.ascontiguousarray(keys, dtype=np.uint64)

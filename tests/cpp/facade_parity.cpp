@@ -168,6 +168,64 @@ int main() {
   std::remove(vp.c_str());
   std::remove(sp.c_str());
 
+  // pointer overloads: find (row addresses), find_or_insert with locked
+  // keys, unlock_keys, lock_keys
+  {
+    float** dptr = nullptr;
+    hipMalloc(&dptr, n * sizeof(float*));
+    table.find(n, dk, dptr, dfound, dsc);
+    hipDeviceSynchronize();
+    auto ptrs = host(dptr, n);
+    auto pf = host(reinterpret_cast<uint8_t*>(dfound), n);
+    std::vector<float> ov2(n * dim, 0.f);
+    std::vector<uint8_t> of2(n);
+    hkvo_find(o, n, keys.data(), ov2.data(), of2.data(), nullptr);
+    REQUIRE(std::memcmp(pf.data(), of2.data(), n) == 0);
+    std::vector<float> row(dim);
+    for (size_t i = 0; i < n; i += 97) {
+      REQUIRE((ptrs[i] != nullptr) == (of2[i] != 0));
+      if (!of2[i]) continue;
+      hipMemcpy(row.data(), ptrs[i], dim * 4, hipMemcpyDefault);
+      REQUIRE(std::memcmp(row.data(), &ov2[i * dim], dim * 4) == 0);
+    }
+    const size_t m = 256;  // the first half was erased above: misses, then hits
+    std::vector<uint64_t> mk(keys.end() - m, keys.end()), msc(m, 7);
+    std::copy(keys.begin(), keys.begin() + m / 2, mk.begin());
+    uint64_t* dmk = dev(mk);
+    uint64_t* dmsc = dev(msc);
+    uint64_t** dkp = nullptr;
+    hipMalloc(&dkp, m * sizeof(uint64_t*));
+    table.find_or_insert(m, dmk, dptr, dfound, dmsc, 0, true, false, dkp);
+    hipDeviceSynchronize();
+    std::vector<uint64_t> oslot(m);
+    std::vector<uint8_t> ofd(m);
+    REQUIRE(hkvo_find_or_insert_ptr(o, m, mk.data(), oslot.data(), ofd.data(), msc.data(), 1, 0,
+                                    1, 0) == 0);
+    auto gfd = host(reinterpret_cast<uint8_t*>(dfound), m);
+    REQUIRE(std::memcmp(gfd.data(), ofd.data(), m) == 0);
+    auto kps = host(dkp, m);
+    for (size_t i = 0; i < m; i++) {
+      REQUIRE((kps[i] != nullptr) == (oslot[i] != HKVO_NO_SLOT));
+      if (!kps[i]) continue;
+      uint64_t w = 0;
+      hipMemcpy(&w, kps[i], 8, hipMemcpyDefault);
+      REQUIRE(w == 0xFFFFFFFFFFFFFFFDull);
+    }
+    table.unlock_keys(m, dkp, dmk, dfound);
+    hipDeviceSynchronize();
+    REQUIRE(hkvo_unlock_keys(o, m, oslot.data(), mk.data(), ofd.data()) == 0);
+    gfd = host(reinterpret_cast<uint8_t*>(dfound), m);
+    REQUIRE(std::memcmp(gfd.data(), ofd.data(), m) == 0);
+    table.lock_keys(m, dmk, dkp, dfound, 0, dmsc);
+    table.unlock_keys(m, dkp, dmk);
+    hipDeviceSynchronize();
+    gfd = host(reinterpret_cast<uint8_t*>(dfound), m);
+    REQUIRE(hkvo_lock_keys(o, m, mk.data(), oslot.data(), ofd.data(), msc.data(), 0) == 0);
+    REQUIRE(std::memcmp(gfd.data(), ofd.data(), m) == 0);
+    REQUIRE(hkvo_unlock_keys(o, m, oslot.data(), mk.data(), nullptr) == 0);
+    REQUIRE(table.size() == hkvo_size(o));
+  }
+
   hkvo_destroy(o);
   std::printf("facade parity ok: %zu keys, %zu exported\n", (size_t)table.size(), c);
   return 0;
