@@ -111,6 +111,13 @@ void launch_find_or_insert_ptr(const TableView& t, const ApplyArgs& a, const Par
 void launch_find_ptr(const TableView& t, const uint64_t* keys, uint64_t n,
                      uint64_t* value_ptrs, uint8_t* founds, uint64_t* scores, bool update,
                      const ScoreCtx& sc, hipStream_t s);
+void launch_contains(const TableView& t, const uint64_t* keys, uint64_t n, uint8_t* founds,
+                     hipStream_t s);
+// assign (with_scores: update_without_missed on each found key) and
+// assign_values: present keys' rows overwritten from `values`.
+void launch_assign(const TableView& t, const uint64_t* keys, uint64_t n, const uint8_t* values,
+                   const uint64_t* scores, bool with_scores, const ScoreCtx& sc, int unit,
+                   hipStream_t s);
 void launch_lock_keys(const TableView& t, const uint64_t* keys, uint64_t n,
                       uint64_t* key_ptrs, uint8_t* success, const uint64_t* scores,
                       const ScoreCtx& sc, hipStream_t s);

@@ -3467,6 +3467,61 @@ __global__ __launch_bounds__(kBlock) void k_unlock_keys(TableView t, uint64_t n,
 }
 
 /* ------------------------------------------------------------------------ */
+/* contains, assign, assign_values                                          */
+/* ------------------------------------------------------------------------ */
+
+// contains (contains_kernel.h:31-69): founds only.
+__global__ __launch_bounds__(kBlock) void k_contains(TableView t, const uint64_t* __restrict__ keys,
+                                                     uint64_t n, uint8_t* __restrict__ founds) {
+  const uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (i >= n) return;
+  const uint64_t k = keys[i];
+  bool found = false;
+  if (!is_reserved(k)) {
+    const KeyPos q = key_pos(t, k);
+    found = probe_find(t, q.b, q.start, q.d, k, false) >= 0;
+  }
+  founds[i] = found ? 1 : 0;
+}
+
+// assign (assign_kernel.h:31-243) and assign_values
+// (assign_values_kernel.h:32-233): a present key's row is overwritten with
+// the input row, and with SCORES its score takes update_without_missed.
+// Absent keys are no-ops.  One key per lane; the wave copies the rows.
+template <bool SCORES, int U>
+__global__ __launch_bounds__(kBlock) void k_assign(TableView t, const uint64_t* __restrict__ keys,
+                                                   uint64_t n, const uint8_t* __restrict__ in_values,
+                                                   const uint64_t* __restrict__ scores,
+                                                   ScoreCtx sc) {
+  __shared__ uint32_t s_rows[kBlock / 64][64];
+  const uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
+  const uint32_t wv = threadIdx.x >> 6;
+  uint64_t src = 0, dst = 0;
+  if (i < n) {
+    const uint64_t k = keys[i];
+    if (!is_reserved(k)) {
+      const KeyPos q = key_pos(t, k);
+      const int p = probe_find(t, q.b, q.start, q.d, k, false);
+      if (p >= 0) {
+        if (SCORES) {
+          const uint64_t g = q.b * t.B + (uint32_t)p;
+          const bool has_in = scores != nullptr;
+          bool w;
+          const uint64_t ns =
+              score_wo_missed(sc, has_in, has_in ? scores[i] : 0, slot_score(t, g), &w);
+          if (w) slot_score(t, g) = ns;
+        }
+        if (in_values) {
+          src = (uint64_t)(uintptr_t)(in_values + i * (uint64_t)t.row_bytes);
+          dst = (uint64_t)(uintptr_t)row_ptr(t, q.b, (uint32_t)p);
+        }
+      }
+    }
+  }
+  wave_copy_pairs<U>(src, dst, t.row_bytes, s_rows[wv]);  // every lane of the wave
+}
+
+/* ------------------------------------------------------------------------ */
 /* export_batch                                                              */
 /* ------------------------------------------------------------------------ */
 
@@ -3852,6 +3907,31 @@ void launch_find_or_insert_ptr(const TableView& t, const ApplyArgs& a0, const Pa
   hipLaunchKernelGGL((k_apply_seq<OP_FIND_OR_INSERT_PTR, 16>), gp, b, 0, s, t, a, ps);
   hipLaunchKernelGGL(k_ptr_finish, dim3(grid_for(a.n, kBlock, 1ull << 31)), b, 0, s, t, a.keys,
                      a.n, ps.trow, vptrs, founds, kptrs, (a.lock && !keep_locked) ? 1 : 0);
+}
+
+void launch_contains(const TableView& t, const uint64_t* keys, uint64_t n, uint8_t* founds,
+                     hipStream_t s) {
+  hipLaunchKernelGGL(k_contains, dim3(grid_for(n, kBlock, 1ull << 31)), dim3(kBlock), 0, s, t,
+                     keys, n, founds);
+}
+
+void launch_assign(const TableView& t, const uint64_t* keys, uint64_t n, const uint8_t* values,
+                   const uint64_t* scores, bool with_scores, const ScoreCtx& sc, int unit,
+                   hipStream_t s) {
+  const dim3 g(grid_for(n, kBlock, 1ull << 31)), b(kBlock);
+#define HKV_ASSIGN_U(UU)                                                                    \
+  if (with_scores)                                                                         \
+    hipLaunchKernelGGL((k_assign<true, UU>), g, b, 0, s, t, keys, n, values, scores, sc);  \
+  else                                                                                     \
+    hipLaunchKernelGGL((k_assign<false, UU>), g, b, 0, s, t, keys, n, values, scores, sc);
+  switch (unit) {
+    case 16: HKV_ASSIGN_U(16); break;
+    case 8: HKV_ASSIGN_U(8); break;
+    case 4: HKV_ASSIGN_U(4); break;
+    case 2: HKV_ASSIGN_U(2); break;
+    default: HKV_ASSIGN_U(1); break;
+  }
+#undef HKV_ASSIGN_U
 }
 
 void launch_find_ptr(const TableView& t, const uint64_t* keys, uint64_t n, uint64_t* vptrs,

@@ -14,6 +14,7 @@
 #include <vector>
 
 #include "../../include/hkv_amd.h"
+#include "../../include/hkv_device_ops.hpp"
 #include "hkv_kernels.h"
 
 using namespace hkv;
@@ -974,6 +975,235 @@ int hkv_set_lru_clock(hkv_table* t, uint64_t clock, int enable) {
     need_table(t);
     t->clock_override = enable != 0;
     t->clock_value = clock;
+  });
+}
+
+}  // extern "C"
+
+namespace {
+
+// Built-in predicates of the C ABI, in the reference's v1 functor form.
+template <class K, class S>
+struct PredScoreLt {
+  __device__ bool operator()(const K&, const S& s, const K&, const S& th) const { return s < th; }
+};
+template <class K, class S>
+struct PredScoreGe {
+  __device__ bool operator()(const K&, const S& s, const K&, const S& th) const { return s >= th; }
+};
+template <class K, class S>
+struct PredScoreGt {
+  __device__ bool operator()(const K&, const S& s, const K&, const S& th) const { return s > th; }
+};
+template <class K, class S>
+struct PredKeyMaskEq {
+  __device__ bool operator()(const K& k, const S&, const K& p, const S&) const {
+    return (k & p) == p;
+  }
+};
+template <class K, class S>
+struct PredKeyLow7GtScoreGt {
+  __device__ bool operator()(const K& k, const S& s, const K& p, const S& th) const {
+    return ((k & 0x7f) > p) && (s > th);
+  }
+};
+
+hkv_device_view device_view(const hkv_table* t) {
+  hkv_device_view v{};
+  v.digests = t->digests;
+  v.slots = t->slots;
+  v.bucket_sizes = t->bsize;
+  v.live = t->live;
+  v.slices = t->d_slices;
+  v.capacity = t->C;
+  v.buckets = t->nb;
+  v.max_bucket_size = (uint32_t)t->B;
+  v.bucket_shift = log2_ceil(t->B);
+  v.slice_shift = (uint32_t)t->slice_shift;
+  v.row_bytes = (uint32_t)t->row;
+  v.reclaim_digest = kReclaimDigest;
+  return v;
+}
+
+// Runs `body.template run<K, V, Pred>()` for the table's key type, a row
+// element type the row size allows, and the predicate kind.
+template <class Body>
+void with_pred(const hkv_table* t, int pred, bool wide_rows, Body&& body) {
+  auto by_k = [&](auto kz) {
+    using K = decltype(kz);
+    auto by_v = [&](auto vz) {
+      using V = decltype(vz);
+      switch (pred) {
+        case HKV_PRED_SCORE_LT: body.template run<K, V, PredScoreLt>(); break;
+        case HKV_PRED_SCORE_GE: body.template run<K, V, PredScoreGe>(); break;
+        case HKV_PRED_SCORE_GT: body.template run<K, V, PredScoreGt>(); break;
+        case HKV_PRED_KEY_MASK_EQ: body.template run<K, V, PredKeyMaskEq>(); break;
+        case HKV_PRED_KEY_LOW7_GT_SCORE_GT: body.template run<K, V, PredKeyLow7GtScoreGt>(); break;
+        default: fail(HKV_ERR_INVALID, "unknown predicate");
+      }
+    };
+    if (wide_rows) by_v(uint32_t{});
+    else by_v(uint8_t{});
+  };
+  if (t->key_type == HKV_KEY_I64) by_k(int64_t{});
+  else by_k(uint64_t{});
+}
+
+struct EraseIfBody {
+  hkv_device_view v;
+  uint64_t pattern, threshold;
+  unsigned long long* d;
+  hipStream_t s;
+  template <class K, class V, template <typename, typename> class P>
+  void run() {
+    hkv_ops::PatternPred<K, V, uint64_t, P> a{(K)pattern, threshold};
+    hip_check(hkv_ops::erase_if<K, V, uint64_t>(v, a, d, s), "erase_if launch");
+  }
+};
+
+struct SizeIfBody {
+  hkv_device_view v;
+  uint64_t pattern, threshold;
+  unsigned long long* d;
+  hipStream_t s;
+  template <class K, class V, template <typename, typename> class P>
+  void run() {
+    hkv_ops::PatternPred<K, V, uint64_t, P> a{(K)pattern, threshold};
+    hip_check(hkv_ops::size_if<K, V, uint64_t>(v, a, d, s), "size_if launch");
+  }
+};
+
+struct ExportIfBody {
+  hkv_device_view v;
+  uint64_t pattern, threshold, n, offset;
+  unsigned long long* d;
+  void* keys;
+  void* values;
+  uint64_t* scores;
+  hipStream_t s;
+  template <class K, class V, template <typename, typename> class P>
+  void run() {
+    hkv_ops::PatternPred<K, V, uint64_t, P> a{(K)pattern, threshold};
+    hip_check(hkv_ops::export_if<K, V, uint64_t>(v, a, n, offset, d, static_cast<K*>(keys),
+                                                 static_cast<V*>(values), scores, s),
+              "export_batch_if launch");
+  }
+};
+
+}  // namespace
+
+extern "C" {
+
+int hkv_set_max_capacity(hkv_table* t, uint64_t new_max_capacity) {
+  return guarded([&] {
+    need_table(t);
+    // include/hkv_hashtable.h:2955-2977
+    if (!ispow2(new_max_capacity))
+      fail(HKV_ERR_UNSUPPORTED, "None power-of-2 new_max_capacity is not supported.");
+    if (new_max_capacity < t->C) return;
+    t->reach_max = false;
+    t->opt.max_capacity = new_max_capacity;
+  });
+}
+
+int hkv_device_view_get(const hkv_table* t, hkv_device_view* out) {
+  return guarded([&] {
+    need_table(t);
+    if (!out) fail(HKV_ERR_INVALID, "null output");
+    *out = device_view(t);
+  });
+}
+
+int hkv_erase_if(hkv_table* t, int pred, uint64_t pattern, uint64_t threshold, hkv_stream stream,
+                 uint64_t* count) {
+  return guarded([&] {
+    need_table(t);
+    // include/hkv_hashtable.h:2409-2441
+    if (!count) fail(HKV_ERR_INVALID, "null count");
+    const hipStream_t s = S(stream);
+    const hkv_device_view v = device_view(t);
+    unsigned long long* d = reinterpret_cast<unsigned long long*>(t->d_sum);
+    launch_fill_u64(t->d_sum, 0, 1, s);
+    EraseIfBody body{v, pattern, threshold, d, s};
+    with_pred(t, pred, false, body);
+    hip_check(hipMemcpyAsync(t->h_sum, t->d_sum, 8, hipMemcpyDeviceToHost, s), "hipMemcpyAsync");
+    hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
+    *count = *t->h_sum;
+  });
+}
+
+int hkv_size_if(hkv_table* t, int pred, uint64_t pattern, uint64_t threshold,
+                uint64_t* d_counter, hkv_stream stream) {
+  return guarded([&] {
+    need_table(t);
+    // include/hkv_hashtable.h:2829-2845
+    if (!d_counter) fail(HKV_ERR_INVALID, "null counter");
+    const hkv_device_view v = device_view(t);
+    SizeIfBody body{v, pattern, threshold, reinterpret_cast<unsigned long long*>(d_counter), S(stream)};
+    with_pred(t, pred, false, body);
+  });
+}
+
+int hkv_export_batch_if(hkv_table* t, int pred, uint64_t pattern, uint64_t threshold, uint64_t n,
+                        uint64_t offset, uint64_t* d_counter, void* keys, void* values,
+                        uint64_t* scores, hkv_stream stream) {
+  return guarded([&] {
+    need_table(t);
+    // include/hkv_hashtable.h:2623-2672
+    if (!d_counter || !keys || !values) fail(HKV_ERR_INVALID, "counter, keys and values must not be null");
+    const hkv_device_view v = device_view(t);
+    const bool wide = (t->row % 4) == 0 && ((uintptr_t)values % 4) == 0;
+    ExportIfBody body{v, pattern, threshold, n, offset, reinterpret_cast<unsigned long long*>(d_counter),
+           keys, values, scores, S(stream)};
+    with_pred(t, pred, wide, body);
+  });
+}
+
+int hkv_assign(hkv_table* t, uint64_t n, const void* keys, const void* values,
+               const uint64_t* scores, hkv_stream stream, int unique_key) {
+  return guarded([&] {
+    need_table(t);
+    // include/hkv_hashtable.h:1830-1921
+    if (n == 0) return;
+    t->check_scores(t->strategy, scores, false);
+    if (!keys || !values) fail(HKV_ERR_INVALID, "keys and values must not be null");
+    const ScoreCtx sc{t->strategy, t->epoch, t->clock_now()};
+    if (!unique_key) {
+      // Scores in batch order through the bucket-owner pipeline, then rows.
+      insert_like(t, OP_ASSIGN_SCORES, n, keys, nullptr, nullptr, scores, nullptr, nullptr,
+                  nullptr, nullptr, nullptr, t->strategy, RULE_DIGEST16, S(stream));
+    }
+    launch_assign(t->view(), reinterpret_cast<const uint64_t*>(keys), n,
+                  reinterpret_cast<const uint8_t*>(values), scores, unique_key != 0, sc,
+                  t->value_unit(values), S(stream));
+    hip_check(hipGetLastError(), "assign launch");
+  });
+}
+
+int hkv_assign_values(hkv_table* t, uint64_t n, const void* keys, const void* values,
+                      hkv_stream stream, int unique_key) {
+  return guarded([&] {
+    need_table(t);
+    // include/hkv_hashtable.h:2003-2093
+    (void)unique_key;
+    if (n == 0) return;
+    if (!keys || !values) fail(HKV_ERR_INVALID, "keys and values must not be null");
+    launch_assign(t->view(), reinterpret_cast<const uint64_t*>(keys), n,
+                  reinterpret_cast<const uint8_t*>(values), nullptr, false, ScoreCtx{},
+                  t->value_unit(values), S(stream));
+    hip_check(hipGetLastError(), "assign_values launch");
+  });
+}
+
+int hkv_contains(hkv_table* t, uint64_t n, const void* keys, uint8_t* founds,
+                 hkv_stream stream) {
+  return guarded([&] {
+    need_table(t);
+    // include/hkv_hashtable.h:2330-2347
+    if (n == 0) return;
+    if (!keys || !founds) fail(HKV_ERR_INVALID, "keys and founds must not be null");
+    launch_contains(t->view(), reinterpret_cast<const uint64_t*>(keys), n, founds, S(stream));
+    hip_check(hipGetLastError(), "contains launch");
   });
 }
 

@@ -19,6 +19,15 @@ LIB_PATH = os.path.join(_HERE, "lib", "libhkv_amd.so")
 HKV_OK, HKV_ERR_INVALID, HKV_ERR_RUNTIME, HKV_ERR_UNSUPPORTED, HKV_ERR_DEVICE = range(5)
 
 
+# Built-in predicates of erase_if / size_if / export_batch_if (the C++
+# facade takes device functors instead).
+PRED_SCORE_LT = 0             # score < threshold
+PRED_SCORE_GE = 1             # score >= threshold
+PRED_SCORE_GT = 2             # score > threshold
+PRED_KEY_MASK_EQ = 3          # (key & pattern) == pattern
+PRED_KEY_LOW7_GT_SCORE_GT = 4  # (key & 0x7f) > pattern and score > threshold
+
+
 class EvictStrategy:
     """include/hkv_hashtable.h:111-119"""
     kLru = 0
@@ -102,6 +111,15 @@ _SIGS = {
     "hkv_assign_scores": [_vp, _u64, _vp, _vp, _vp, _i32],
     "hkv_find": [_vp, _u64, _vp, _vp, _vp, _vp, _vp],
     "hkv_find_missed": [_vp, _u64, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
+    "hkv_assign": [_vp, _u64, _vp, _vp, _vp, _vp, _i32],
+    "hkv_assign_values": [_vp, _u64, _vp, _vp, _vp, _i32],
+    "hkv_contains": [_vp, _u64, _vp, _vp, _vp],
+    "hkv_erase_if": [_vp, _i32, _u64, _u64, _vp, ctypes.POINTER(_u64)],
+    "hkv_size_if": [_vp, _i32, _u64, _u64, _vp, _vp],
+    "hkv_export_batch_if": [_vp, _i32, _u64, _u64, _u64, _u64, _vp, _vp, _vp, _vp,
+                            _vp],
+    "hkv_set_max_capacity": [_vp, _u64],
+    "hkv_device_view_get": [_vp, _vp],
     "hkv_find_ptr": [_vp, _u64, _vp, _vp, _vp, _vp, _vp, _i32],
     "hkv_find_and_update": [_vp, _u64, _vp, _vp, _vp, _vp, _vp, _i32],
     "hkv_find_or_insert_ptr": [_vp, _u64, _vp, _vp, _vp, _vp, _vp, _i32, _i32,
@@ -317,7 +335,22 @@ class HashTable:
         _check(_LIB.hkv_assign_scores(self._h, n, _ptr(keys), _ptr(scores),
                                       _stream(stream), int(unique_key)))
 
+    def assign(self, n, keys, values, scores=None, stream=0, unique_key=True):
+        """include/hkv_hashtable.h:1830-1921."""
+        _check(_LIB.hkv_assign(self._h, n, _ptr(keys), _ptr(values), _ptr(scores),
+                               _stream(stream), int(unique_key)))
+
+    def assign_values(self, n, keys, values, stream=0, unique_key=True):
+        """include/hkv_hashtable.h:2003-2093."""
+        _check(_LIB.hkv_assign_values(self._h, n, _ptr(keys), _ptr(values),
+                                      _stream(stream), int(unique_key)))
+
     # --- lookups -------------------------------------------------------------
+    def contains(self, n, keys, founds, stream=0):
+        """include/hkv_hashtable.h:2330-2347."""
+        _check(_LIB.hkv_contains(self._h, n, _ptr(keys), _ptr(founds),
+                                 _stream(stream)))
+
     def find(self, n, keys, values, founds, scores=None, stream=0):
         _check(_LIB.hkv_find(self._h, n, _ptr(keys), _ptr(values),
                              _ptr(founds), _ptr(scores), _stream(stream)))
@@ -379,6 +412,33 @@ class HashTable:
         _check(_LIB.hkv_slot_addresses(self._h, sl.size, sl.ctypes.data,
                                        kp.ctypes.data, vp.ctypes.data))
         return kp, vp
+
+    # --- predicates (built-in predicate kinds, PRED_*) ------------------------
+    def erase_if(self, pred, pattern, threshold, stream=0):
+        """include/hkv_hashtable.h:2409-2441; returns the number erased."""
+        out = ctypes.c_uint64()
+        _check(_LIB.hkv_erase_if(self._h, pred, pattern, threshold, _stream(stream),
+                                 ctypes.byref(out)))
+        return out.value
+
+    def size_if(self, pred, pattern, threshold, d_counter, stream=0):
+        """include/hkv_hashtable.h:2829-2845; the count lands in d_counter."""
+        _check(_LIB.hkv_size_if(self._h, pred, pattern, threshold, _ptr(d_counter),
+                                _stream(stream)))
+
+    def export_batch_if(self, pred, pattern, threshold, n, offset, d_counter, keys,
+                        values, scores=None, stream=0):
+        """include/hkv_hashtable.h:2623-2672; tuple order is unspecified."""
+        _check(_LIB.hkv_export_batch_if(self._h, pred, pattern, threshold, n, offset,
+                                        _ptr(d_counter), _ptr(keys), _ptr(values),
+                                        _ptr(scores), _stream(stream)))
+
+    def empty(self, stream=0):
+        return self.size(stream) == 0
+
+    def set_max_capacity(self, new_max_capacity):
+        """include/hkv_hashtable.h:2955-2977."""
+        _check(_LIB.hkv_set_max_capacity(self._h, new_max_capacity))
 
     # --- maintenance ---------------------------------------------------------
     def erase(self, n, keys, stream=0):

@@ -23,9 +23,18 @@
  *                               include/hkv_hashtable.h:1658-1728
  *   HashTable::lock_keys        include/hkv_hashtable.h:1744-1771
  *   HashTable::unlock_keys      include/hkv_hashtable.h:1788-1804
+ *   HashTable::assign           include/hkv_hashtable.h:1830-1921
  *   HashTable::assign_scores    include/hkv_hashtable.h:1943-1977
+ *   HashTable::assign_values    include/hkv_hashtable.h:2003-2093
+ *   HashTable::contains         include/hkv_hashtable.h:2330-2347
  *   HashTable::find             include/hkv_hashtable.h:2113-2152
  *   HashTable::find (missed)    include/hkv_hashtable.h:2175-2220
+ *   HashTable::erase_if / erase_if_v2
+ *                               include/hkv_hashtable.h:2409-2470
+ *   HashTable::export_batch_if / export_batch_if_v2
+ *                               include/hkv_hashtable.h:2623-2735
+ *   HashTable::for_each         include/hkv_hashtable.h:2755-2772
+ *   HashTable::size_if          include/hkv_hashtable.h:2829-2845
  *   HashTable::find (pointers)  include/hkv_hashtable.h:2244-2262
  *   HashTable::find_and_update  include/hkv_hashtable.h:2288-2317
  *   HashTable::erase            include/hkv_hashtable.h:2358-2376
@@ -34,6 +43,7 @@
  *   HashTable::size             include/hkv_hashtable.h:2792-2819
  *   HashTable::reserve          include/hkv_hashtable.h:2873-2935
  *   HashTable::load_factor      include/hkv_hashtable.h:2945-2947
+ *   HashTable::set_max_capacity include/hkv_hashtable.h:2955-2977
  *   HashTable::set_global_epoch include/hkv_hashtable.h:3197
  *   HashTable::save / load      include/hkv_hashtable.h:3021-3195
  *   BaseKVFile / LocalKVFile    include/types.h:291-464
@@ -142,6 +152,22 @@ int hkv_assign_scores(hkv_table* t, uint64_t n, const void* keys,
                       const uint64_t* scores, hkv_stream stream,
                       int unique_key);
 
+/* assign: present keys take the input row and update_without_missed on
+ * their score (the assign_scores functor); absent keys are no-ops.  With
+ * unique_key=0 the scores apply in batch order and, for a repeated key, the
+ * row of one of its occurrences lands (unspecified which, as in the
+ * reference). */
+int hkv_assign(hkv_table* t, uint64_t n, const void* keys, const void* values,
+               const uint64_t* scores, hkv_stream stream, int unique_key);
+
+/* assign_values: present keys take the input row; scores are untouched. */
+int hkv_assign_values(hkv_table* t, uint64_t n, const void* keys,
+                      const void* values, hkv_stream stream, int unique_key);
+
+/* contains: founds only. */
+int hkv_contains(hkv_table* t, uint64_t n, const void* keys, uint8_t* founds,
+                 hkv_stream stream);
+
 /* Missed rows of `values` are left untouched; `scores` may be NULL. */
 int hkv_find(hkv_table* t, uint64_t n, const void* keys, void* values,
              uint8_t* founds, uint64_t* scores, hkv_stream stream);
@@ -198,6 +224,58 @@ int hkv_unlock_keys(hkv_table* t, uint64_t n, void* const* locked_key_ptrs,
                     const void* keys, uint8_t* success, hkv_stream stream);
 
 int hkv_erase(hkv_table* t, uint64_t n, const void* keys, hkv_stream stream);
+
+/* Predicate APIs.  The reference takes the caller's device functor; the C++
+ * facade does too (hkv_device_ops.hpp instantiates its kernels with it).  An
+ * FFI caller picks one of these built-in predicates on (key, score), with
+ * the table's key type:                                                    */
+enum {
+  HKV_PRED_SCORE_LT = 0,      /* score <  threshold                          */
+  HKV_PRED_SCORE_GE = 1,      /* score >= threshold                          */
+  HKV_PRED_SCORE_GT = 2,      /* score >  threshold                          */
+  HKV_PRED_KEY_MASK_EQ = 3,   /* (key & pattern) == pattern                  */
+  HKV_PRED_KEY_LOW7_GT_SCORE_GT = 4, /* (key & 0x7f) > pattern && score > threshold */
+};
+
+/* erase_if: matching live slots become RECLAIM.  Synchronous; `count` (host)
+ * receives the number erased. */
+int hkv_erase_if(hkv_table* t, int pred, uint64_t pattern, uint64_t threshold,
+                 hkv_stream stream, uint64_t* count);
+
+/* size_if: `d_counter` (device uint64) receives the number of matches. */
+int hkv_size_if(hkv_table* t, int pred, uint64_t pattern, uint64_t threshold,
+                uint64_t* d_counter, hkv_stream stream);
+
+/* export_batch_if: matching live slots of [offset, offset + n), appended in
+ * an unspecified order; `d_counter` (device uint64) receives the count. */
+int hkv_export_batch_if(hkv_table* t, int pred, uint64_t pattern,
+                        uint64_t threshold, uint64_t n, uint64_t offset,
+                        uint64_t* d_counter, void* keys, void* values,
+                        uint64_t* scores, hkv_stream stream);
+
+/* Raw device view of a table, for the predicate and traversal kernels that
+ * callers instantiate with their own functors (hkv_device_ops.hpp).  It
+ * stands for the reference's Table<K, V, S> members those kernels read
+ * (include/types.h:173-248).  Slot g = bucket * max_bucket_size + slot;
+ * its key is slots[2g], its score slots[2g + 1]; its row is in
+ * slices[bucket >> slice_shift] at ((bucket & ((1 << slice_shift) - 1)) *
+ * max_bucket_size + slot) * row_bytes.  Valid until the table grows or is
+ * destroyed. */
+typedef struct hkv_device_view {
+  uint8_t* digests;
+  uint64_t* slots;
+  int32_t* bucket_sizes;
+  uint64_t* live;           /* live-key counter kept by every kernel */
+  uint8_t* const* slices;   /* device array of value-slice base addresses */
+  uint64_t capacity;
+  uint64_t buckets;
+  uint32_t max_bucket_size;
+  uint32_t bucket_shift;
+  uint32_t slice_shift;
+  uint32_t row_bytes;
+  uint8_t reclaim_digest;
+} hkv_device_view;
+int hkv_device_view_get(const hkv_table* t, hkv_device_view* out);
 int hkv_clear(hkv_table* t, hkv_stream stream);
 
 /* Exports live slots [offset, offset + n) in slot order; `d_counter`
@@ -208,6 +286,10 @@ int hkv_export_batch(hkv_table* t, uint64_t n, uint64_t offset,
 
 /* Synchronous. */
 int hkv_reserve(hkv_table* t, uint64_t new_capacity, hkv_stream stream);
+
+/* set_max_capacity: a power of 2 (invalid_argument otherwise); below the
+ * current capacity it does nothing. */
+int hkv_set_max_capacity(hkv_table* t, uint64_t new_max_capacity);
 /* Key-value files (include/types.h:291-464, BaseKVFile / LocalKVFile): a
  * file is a pair of callbacks over `ctx`.  `row_bytes` = dim * sizeof(V);
  * each returns the number of records read or written. */

@@ -16,8 +16,30 @@
 
 #include "hkv_amd.h"
 
+#if defined(__HIPCC__)
+// Predicate and traversal APIs take device functors: with hipcc their
+// kernels are instantiated here from hkv_device_ops.hpp.  The reference's
+// functors compile unchanged: its device-function and global-memory
+// qualifiers map to HIP's.
+#include "hkv_device_ops.hpp"
+#ifndef __simt_callee__
+#define __simt_callee__ __device__
+#endif
+#ifndef __gm__
+#define __gm__
+#endif
+#endif
+
 namespace npu {
 namespace hkv {
+
+#if defined(__HIPCC__)
+// include/types.h:67,153-156: the four reserved key values.
+template <class K>
+__host__ __device__ inline bool IS_RESERVED_KEY(K key) {
+  return hkv_ops::is_reserved_word(static_cast<uint64_t>(key));
+}
+#endif
 
 using aclrtStream = hipStream_t;
 
@@ -59,6 +81,10 @@ class HkvException : public std::runtime_error {
 };
 
 namespace detail {
+
+inline void hip(hipError_t e) {
+  if (e != hipSuccess) throw NpuException(hipGetErrorString(e));
+}
 
 inline void check(int rc) {
   if (rc == HKV_OK) return;
@@ -244,6 +270,27 @@ class HashTable {
                                   reinterpret_cast<uint8_t*>(success), stream));
   }
 
+  void assign(size_type n, const key_type* keys, const value_type* values,
+              const score_type* scores = nullptr, aclrtStream stream = 0,
+              bool unique_key = true) {
+    detail::check(hkv_assign(t_, n, keys, values, scores, stream, unique_key));
+  }
+
+  // Alias of assign_scores, as in the reference.
+  void assign(size_type n, const key_type* keys, const score_type* scores = nullptr,
+              aclrtStream stream = 0, bool unique_key = true) {
+    assign_scores(n, keys, scores, stream, unique_key);
+  }
+
+  void assign_values(size_type n, const key_type* keys, const value_type* values,
+                     aclrtStream stream = 0, bool unique_key = true) {
+    detail::check(hkv_assign_values(t_, n, keys, values, stream, unique_key));
+  }
+
+  void contains(size_type n, const key_type* keys, bool* founds, aclrtStream stream = 0) const {
+    detail::check(hkv_contains(t_, n, keys, reinterpret_cast<uint8_t*>(founds), stream));
+  }
+
   void assign_scores(size_type n, const key_type* keys, const score_type* scores = nullptr,
                      aclrtStream stream = 0, bool unique_key = true) {
     detail::check(hkv_assign_scores(t_, n, keys, scores, stream, unique_key));
@@ -276,6 +323,86 @@ class HashTable {
                                       reinterpret_cast<uint8_t*>(founds), scores, stream,
                                       unique_key));
   }
+
+#if defined(__HIPCC__)
+  // include/hkv_hashtable.h:2409-2441: PredFunctor<K, S>{}(key, score,
+  // pattern, threshold) selects the live slots to erase.
+  template <template <typename, typename> class PredFunctor>
+  size_type erase_if(const key_type& pattern, const score_type& threshold,
+                     aclrtStream stream = 0) {
+    hkv_device_view v;
+    detail::check(hkv_device_view_get(t_, &v));
+    size_type* d = counter();
+    zero_counter(d, stream);
+    hkv_ops::PatternPred<K, V, S, PredFunctor> a{pattern, threshold};
+    detail::hip(hkv_ops::erase_if<K, V, S>(v, a, reinterpret_cast<unsigned long long*>(d),
+                                           stream));
+    return read_counter(d, stream);
+  }
+
+  // include/hkv_hashtable.h:2447-2470: pred(key, row, score, group_size).
+  template <typename PredFunctor>
+  size_type erase_if_v2(PredFunctor& pred, aclrtStream stream = 0) {
+    hkv_device_view v;
+    detail::check(hkv_device_view_get(t_, &v));
+    size_type* d = counter();
+    zero_counter(d, stream);
+    hkv_ops::RowPred<K, V, S, PredFunctor> a{pred};
+    detail::hip(hkv_ops::erase_if<K, V, S>(v, a, reinterpret_cast<unsigned long long*>(d),
+                                           stream));
+    return read_counter(d, stream);
+  }
+
+  // include/hkv_hashtable.h:2623-2672 (order of the exported tuples is
+  // unspecified, as in the reference).
+  template <template <typename, typename> class PredFunctor>
+  void export_batch_if(const key_type& pattern, const score_type& threshold, size_type n,
+                       const size_type offset, size_type* d_counter, key_type* keys,
+                       value_type* values, score_type* scores = nullptr,
+                       aclrtStream stream = 0) const {
+    hkv_device_view v;
+    detail::check(hkv_device_view_get(t_, &v));
+    hkv_ops::PatternPred<K, V, S, PredFunctor> a{pattern, threshold};
+    detail::hip(hkv_ops::export_if<K, V, S>(v, a, n, offset,
+                                            reinterpret_cast<unsigned long long*>(d_counter),
+                                            keys, values, scores, stream));
+  }
+
+  // include/hkv_hashtable.h:2693-2735: pred.operator()<group_size>(key, row,
+  // score).
+  template <typename PredFunctor>
+  void export_batch_if_v2(PredFunctor& pred, size_type n, const size_type offset,
+                          size_type* d_counter, key_type* keys, value_type* values,
+                          score_type* scores = nullptr, aclrtStream stream = 0) const {
+    hkv_device_view v;
+    detail::check(hkv_device_view_get(t_, &v));
+    hkv_ops::RowPredT<K, V, S, PredFunctor> a{pred};
+    detail::hip(hkv_ops::export_if<K, V, S>(v, a, n, offset,
+                                            reinterpret_cast<unsigned long long*>(d_counter),
+                                            keys, values, scores, stream));
+  }
+
+  // include/hkv_hashtable.h:2755-2772: f(key, row, &score, group_size) on
+  // every slot of [first, last).
+  template <typename ExecutionFunc>
+  void for_each(const size_type first, const size_type last, ExecutionFunc& f,
+                aclrtStream stream = 0) {
+    hkv_device_view v;
+    detail::check(hkv_device_view_get(t_, &v));
+    detail::hip(hkv_ops::for_each<K, V, S>(v, f, first, last, stream));
+  }
+
+  // include/hkv_hashtable.h:2829-2845.
+  template <template <typename, typename> class PredFunctor>
+  void size_if(const key_type& pattern, const score_type& threshold, size_type* d_counter,
+               aclrtStream stream = 0) const {
+    hkv_device_view v;
+    detail::check(hkv_device_view_get(t_, &v));
+    hkv_ops::PatternPred<K, V, S, PredFunctor> a{pattern, threshold};
+    detail::hip(hkv_ops::size_if<K, V, S>(v, a, reinterpret_cast<unsigned long long*>(d_counter),
+                                          stream));
+  }
+#endif
 
   void erase(size_type n, const key_type* keys, aclrtStream stream = 0) {
     detail::check(hkv_erase(t_, n, keys, stream));
@@ -332,6 +459,14 @@ class HashTable {
     detail::check(hkv_load_factor(t_, stream, &f));
     return f;
   }
+  // include/hkv_hashtable.h:2784
+  bool empty(aclrtStream stream = 0) const { return size(stream) == 0; }
+
+  // include/hkv_hashtable.h:2955-2977
+  void set_max_capacity(size_type new_max_capacity) {
+    detail::check(hkv_set_max_capacity(t_, new_max_capacity));
+  }
+
   size_type capacity() const { return hkv_capacity(t_); }
   size_type dim() const noexcept { return hkv_dim(t_); }
   size_type max_bucket_size() const noexcept { return hkv_max_bucket_size(t_); }

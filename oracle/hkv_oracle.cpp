@@ -871,6 +871,58 @@ int hkvo_find(hkvo_table* t, uint64_t n, const uint64_t* keys, void* values,
   return HKVO_OK;
 }
 
+int hkvo_contains(hkvo_table* t, uint64_t n, const uint64_t* keys,
+                  uint8_t* founds) {
+  // include/kernels/contains_kernel/contains_kernel.h:31-69
+  for (uint64_t i = 0; i < n; i++) {
+    const uint64_t k = keys[i];
+    bool found = false;
+    if (!is_reserved(k)) {
+      uint64_t b;
+      uint32_t s;
+      uint8_t d;
+      t->locate_key(k, &b, &s, &d);
+      found = t->find_slot(b, s, d, k) >= 0;
+    }
+    founds[i] = found ? 1 : 0;
+  }
+  return HKVO_OK;
+}
+
+int hkvo_assign(hkvo_table* t, uint64_t n, const uint64_t* keys,
+                const void* values, const uint64_t* scores, int with_scores,
+                uint64_t clock) {
+  // assign (include/hkv_hashtable.h:1830-1921, assign_kernel.h:31-243) with
+  // with_scores, assign_values (include/hkv_hashtable.h:2003-2093,
+  // assign_values_kernel.h:32-233) without: batch order, a present key takes
+  // the input row and, for assign, update_without_missed on its score.
+  if (n == 0) return HKVO_OK;
+  if (with_scores) {
+    int rc = t->check(t->strategy, scores, false);
+    if (rc) return rc;
+  }
+  const bool has_in = scores != nullptr;
+  for (uint64_t i = 0; i < n; i++) {
+    const uint64_t k = keys[i];
+    if (is_reserved(k)) continue;
+    uint64_t b;
+    uint32_t s;
+    uint8_t d;
+    t->locate_key(k, &b, &s, &d);
+    const int64_t p = t->find_slot(b, s, d, k);
+    if (p < 0) continue;
+    if (with_scores) {
+      bool w;
+      const uint64_t g = b * t->B + (uint64_t)p;
+      const uint64_t ns = score_wo_missed(t->strategy, has_in, has_in ? scores[i] : 0,
+                                          t->epoch, clock, t->scores[g], &w);
+      if (w) t->scores[g] = ns;
+    }
+    std::memcpy(t->rowp(b, (uint32_t)p), (const uint8_t*)values + i * t->row, t->row);
+  }
+  return HKVO_OK;
+}
+
 int hkvo_find_ptr(hkvo_table* t, uint64_t n, const uint64_t* keys,
                   uint64_t* slots, uint8_t* founds, uint64_t* scores) {
   // include/kernels/find_ptr_kernel/find_ptr_with_digest_kernel.h:30-148
@@ -1039,6 +1091,86 @@ int hkvo_find_missed(hkvo_table* t, uint64_t n, const uint64_t* keys,
     }
   }
   *missed_size = m;
+  return HKVO_OK;
+}
+
+// Built-in predicates of erase_if / size_if / export_batch_if, in the
+// reference's v1 functor form PredFunctor<K, S>(key, score, pattern,
+// threshold) (include/hkv_hashtable.h:2380-2398); key_signed selects K =
+// int64_t.
+static bool pred_eval(int pred, int key_signed, uint64_t k, uint64_t s, uint64_t pat,
+                      uint64_t th) {
+  switch (pred) {
+    case 0: return s < th;
+    case 1: return s >= th;
+    case 2: return s > th;
+    case 3: return (k & pat) == pat;
+    case 4:
+      if (key_signed) return ((int64_t)(k & 0x7f) > (int64_t)pat) && (s > th);
+      return ((k & 0x7f) > pat) && (s > th);
+    default: return false;
+  }
+}
+
+int hkvo_erase_if(hkvo_table* t, int pred, uint64_t pattern, uint64_t threshold,
+                  int key_signed, uint64_t* count) {
+  // remove_if_kernel (include/kernels/remove_kernel/remove_kernel.h:116-160)
+  if (pred < 0 || pred > 4) return HKVO_ERR_INVALID;
+  uint64_t c = 0;
+  for (uint64_t g = 0; g < t->C; g++) {
+    const uint64_t k = t->keys[g];
+    if (is_reserved(k)) continue;
+    if (!pred_eval(pred, key_signed, k, t->scores[g], pattern, threshold)) continue;
+    t->keys[g] = RECLAIM_KEY;
+    t->scores[g] = EMPTY_SCORE;
+    t->dg[g] = t->reclaim_d;
+    t->bsize[g / t->B]--;
+    c++;
+  }
+  *count = c;
+  return HKVO_OK;
+}
+
+int hkvo_size_if(hkvo_table* t, int pred, uint64_t pattern, uint64_t threshold,
+                 int key_signed, uint64_t* count) {
+  // size_if_kernel (include/kernels/size_if_kernel/size_if_kernel.h)
+  if (pred < 0 || pred > 4) return HKVO_ERR_INVALID;
+  uint64_t c = 0;
+  for (uint64_t g = 0; g < t->C; g++) {
+    const uint64_t k = t->keys[g];
+    if (!is_reserved(k) && pred_eval(pred, key_signed, k, t->scores[g], pattern, threshold)) c++;
+  }
+  *count = c;
+  return HKVO_OK;
+}
+
+uint64_t hkvo_export_batch_if(hkvo_table* t, int pred, uint64_t pattern,
+                              uint64_t threshold, int key_signed, uint64_t n,
+                              uint64_t offset, uint64_t* keys, void* values,
+                              uint64_t* scores) {
+  // dump_kernel_if (include/kernels/dump_kernel/dump_kernel_if.h), listed in
+  // slot order (the device order is unspecified).
+  if (offset >= t->C) return 0;
+  n = std::min(n, t->C - offset);
+  uint64_t c = 0;
+  for (uint64_t g = offset; g < offset + n; g++) {
+    const uint64_t k = t->keys[g];
+    if (is_reserved(k) || !pred_eval(pred, key_signed, k, t->scores[g], pattern, threshold))
+      continue;
+    keys[c] = k;
+    if (scores) scores[c] = t->scores[g];
+    std::memcpy((uint8_t*)values + c * t->row, t->rowp(g / t->B, (uint32_t)(g % t->B)), t->row);
+    c++;
+  }
+  return c;
+}
+
+int hkvo_set_max_capacity(hkvo_table* t, uint64_t new_max) {
+  // include/hkv_hashtable.h:2955-2977
+  if (new_max == 0 || (new_max & (new_max - 1))) return HKVO_ERR_UNSUPPORTED;
+  if (new_max < t->C) return HKVO_OK;
+  t->reach_max = false;
+  t->max_cap = new_max;
   return HKVO_OK;
 }
 

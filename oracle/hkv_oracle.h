@@ -68,6 +68,12 @@ int hkvo_accum_or_assign(hkvo_table* t, uint64_t n, const uint64_t* keys,
                          uint64_t clock);
 int hkvo_assign_scores(hkvo_table* t, uint64_t n, const uint64_t* keys,
                        const uint64_t* scores, uint64_t clock);
+int hkvo_contains(hkvo_table* t, uint64_t n, const uint64_t* keys,
+                  uint8_t* founds);
+/* assign (with_scores = 1) and assign_values (with_scores = 0). */
+int hkvo_assign(hkvo_table* t, uint64_t n, const uint64_t* keys,
+                const void* values, const uint64_t* scores, int with_scores,
+                uint64_t clock);
 /* Pointer APIs: slot indices (bucket * B + slot) stand for the addresses the
  * product returns; HKVO_NO_SLOT for none. */
 #define HKVO_NO_SLOT 0xFFFFFFFFFFFFFFFFull
@@ -86,6 +92,17 @@ int hkvo_lock_keys(hkvo_table* t, uint64_t n, const uint64_t* keys,
 int hkvo_unlock_keys(hkvo_table* t, uint64_t n, const uint64_t* slots,
                      const uint64_t* keys, uint8_t* success);
 int hkvo_erase(hkvo_table* t, uint64_t n, const uint64_t* keys);
+/* Predicate APIs with the product's built-in predicate kinds (HKV_PRED_*);
+ * key_signed selects int64 keys.  export lists in slot order. */
+int hkvo_erase_if(hkvo_table* t, int pred, uint64_t pattern, uint64_t threshold,
+                  int key_signed, uint64_t* count);
+int hkvo_size_if(hkvo_table* t, int pred, uint64_t pattern, uint64_t threshold,
+                 int key_signed, uint64_t* count);
+uint64_t hkvo_export_batch_if(hkvo_table* t, int pred, uint64_t pattern,
+                              uint64_t threshold, int key_signed, uint64_t n,
+                              uint64_t offset, uint64_t* keys, void* values,
+                              uint64_t* scores);
+int hkvo_set_max_capacity(hkvo_table* t, uint64_t new_max_capacity);
 void hkvo_clear(hkvo_table* t);
 uint64_t hkvo_export_batch(hkvo_table* t, uint64_t n, uint64_t offset,
                            uint64_t* keys, void* values, uint64_t* scores);

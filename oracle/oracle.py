@@ -94,6 +94,19 @@ def lib():
                                                 ctypes.c_uint64,
                                                 ctypes.c_uint64,
                                                 ctypes.c_uint64]
+        L.hkvo_erase_if.argtypes = [vp, ctypes.c_int, ctypes.c_uint64,
+                                    ctypes.c_uint64, ctypes.c_int, vp]
+        L.hkvo_size_if.argtypes = [vp, ctypes.c_int, ctypes.c_uint64,
+                                   ctypes.c_uint64, ctypes.c_int, vp]
+        L.hkvo_export_batch_if.restype = ctypes.c_uint64
+        L.hkvo_export_batch_if.argtypes = [vp, ctypes.c_int, ctypes.c_uint64,
+                                           ctypes.c_uint64, ctypes.c_int,
+                                           ctypes.c_uint64, ctypes.c_uint64,
+                                           vp, vp, vp]
+        L.hkvo_set_max_capacity.argtypes = [vp, ctypes.c_uint64]
+        L.hkvo_contains.argtypes = [vp, ctypes.c_uint64, vp, vp]
+        L.hkvo_assign.argtypes = [vp, ctypes.c_uint64, vp, vp, vp, ctypes.c_int,
+                                  ctypes.c_uint64]
         L.hkvo_find_ptr.argtypes = [vp, ctypes.c_uint64, vp, vp, vp, vp]
         L.hkvo_find_and_update.argtypes = [vp, ctypes.c_uint64, vp, vp, vp, vp,
                                            ctypes.c_int, ctypes.c_uint64]
@@ -239,6 +252,51 @@ class Oracle:
         s = None if scores is None else np.ascontiguousarray(scores, np.uint64)
         _chk(lib().hkvo_assign_scores(self.h, keys.size, _p(keys), _p(s),
                                       clock))
+
+    # --- predicates: built-in kinds 0..4 (see include/hkv_amd.h) -----------
+    def erase_if(self, pred, pattern, threshold, key_signed=False):
+        c = np.zeros(1, np.uint64)
+        _chk(lib().hkvo_erase_if(self.h, pred, pattern, threshold,
+                                 int(key_signed), _p(c)))
+        return int(c[0])
+
+    def size_if(self, pred, pattern, threshold, key_signed=False):
+        c = np.zeros(1, np.uint64)
+        _chk(lib().hkvo_size_if(self.h, pred, pattern, threshold,
+                                int(key_signed), _p(c)))
+        return int(c[0])
+
+    def export_batch_if(self, pred, pattern, threshold, n, offset=0,
+                        key_signed=False):
+        cap = self.capacity()
+        m = max(0, min(n, cap - offset)) if offset < cap else 0
+        k = np.zeros(m, np.uint64)
+        v = np.zeros((m, self.dim), self.np_vt)
+        s = np.zeros(m, np.uint64)
+        c = lib().hkvo_export_batch_if(self.h, pred, pattern, threshold,
+                                       int(key_signed), n, offset, _p(k), _p(v),
+                                       _p(s))
+        return k[:c], v[:c], s[:c]
+
+    def set_max_capacity(self, new_max):
+        _chk(lib().hkvo_set_max_capacity(self.h, new_max))
+
+    def contains(self, keys):
+        keys = np.ascontiguousarray(keys, dtype=np.uint64)
+        f = np.zeros(keys.size, np.uint8)
+        _chk(lib().hkvo_contains(self.h, keys.size, _p(keys), _p(f)))
+        return f.astype(bool)
+
+    def assign(self, keys, values, scores=None, clock=0):
+        keys = np.ascontiguousarray(keys, dtype=np.uint64)
+        v = self._vals(values, keys.size)
+        s = None if scores is None else np.ascontiguousarray(scores, np.uint64)
+        _chk(lib().hkvo_assign(self.h, keys.size, _p(keys), _p(v), _p(s), 1, clock))
+
+    def assign_values(self, keys, values):
+        keys = np.ascontiguousarray(keys, dtype=np.uint64)
+        v = self._vals(values, keys.size)
+        _chk(lib().hkvo_assign(self.h, keys.size, _p(keys), _p(v), None, 0, 0))
 
     # --- pointer APIs: global slot indices (NO_SLOT for none) ----------------
     def find_ptr(self, keys, with_scores=False):

@@ -229,3 +229,100 @@ def test_keep_locked_requires_unique_keys():
                              np.ones(4, np.uint64), unique_key=False,
                              keep_locked=True)
     assert e.value.code == 3
+
+
+@pytest.mark.parametrize("strategy", [O.LFU, O.CUSTOMIZED, O.LRU, O.EPOCH_LFU])
+def test_assign_contains_closed_forms(strategy):
+    # contains = find's founds; assign = assign_scores (pinned separately)
+    # plus the input row on present keys; assign_values = the row only.
+    rng = np.random.default_rng(31)
+    mk = lambda: O.Oracle(1 << 12, dim=4, strategy=strategy)
+    a, b, c = mk(), mk(), mk()
+    for t in (a, b, c):
+        t.set_global_epoch(2)
+    ks = uniform_keys(rng, 1500)
+    sc = None if strategy == O.LRU else rng.integers(1, 1 << 30, size=ks.size,
+                                                      dtype=np.uint64)
+    for t in (a, b, c):
+        t.insert_or_assign(ks, values_for(ks, 4), sc, clock=10)
+    q = np.concatenate([ks[:800], uniform_keys(rng, 400, exclude=ks),
+                        np.array([0xFFFFFFFFFFFFFFFF], np.uint64)])
+    _, f, _ = a.find(q)
+    np.testing.assert_array_equal(a.contains(q), f)
+    inp = None if strategy == O.LRU else rng.integers(1, 1 << 30, size=q.size,
+                                                      dtype=np.uint64)
+    rows = rng.standard_normal((q.size, 4)).astype(np.float32)
+    a.assign(q, rows, inp, clock=99)
+    b.assign_scores(q, inp, clock=99)
+    c.assign_values(q, rows)
+    _, ka, sa, ba, va = a.raw()
+    _, kb, sb, bb, vb = b.raw()
+    _, kc, scc, bc, vc = c.raw()
+    np.testing.assert_array_equal(ka, kb)
+    np.testing.assert_array_equal(sa, sb)
+    np.testing.assert_array_equal(ba, bb)
+    np.testing.assert_array_equal(va, vc)
+    got, found, _ = a.find(q)
+    np.testing.assert_array_equal(got[found], rows[found])
+    assert a.size() == 1500
+    # assign_values leaves scores as inserted
+    x = O.Oracle(1 << 12, dim=4, strategy=strategy)
+    x.set_global_epoch(2)
+    x.insert_or_assign(ks, values_for(ks, 4), sc, clock=10)
+    np.testing.assert_array_equal(scc, x.raw()[2])
+
+
+def _np_pred(kind, k, s, pat, th):
+    if kind == 0:
+        return s < np.uint64(th)
+    if kind == 1:
+        return s >= np.uint64(th)
+    if kind == 2:
+        return s > np.uint64(th)
+    if kind == 3:
+        return (k & np.uint64(pat)) == np.uint64(pat)
+    return ((k & np.uint64(0x7F)) > np.uint64(pat)) & (s > np.uint64(th))
+
+
+@pytest.mark.parametrize("kind,pat,th", [(0, 0, 500), (1, 0, 500), (2, 0, 900),
+                                         (3, 0x5, 0), (4, 0x3F, 300)])
+def test_predicate_apis_closed_forms(kind, pat, th):
+    # size_if / export_batch_if / erase_if against the same predicate
+    # evaluated by numpy over the full export (include/hkv_hashtable.h:
+    # 2409-2441, 2623-2672, 2829-2845).
+    rng = np.random.default_rng(40 + kind)
+    t = O.Oracle(1 << 13, dim=4, strategy=O.CUSTOMIZED)
+    ks = uniform_keys(rng, 3000)
+    sc = rng.integers(0, 1000, size=ks.size, dtype=np.uint64)
+    t.insert_or_assign(ks, values_for(ks, 4), sc)
+    k, v, s = t.export_batch(1 << 13)
+    m = _np_pred(kind, k, s, pat, th)
+    assert t.size_if(kind, pat, th) == int(m.sum())
+    ek, ev, es = t.export_batch_if(kind, pat, th, 1 << 13)
+    np.testing.assert_array_equal(ek, k[m])
+    np.testing.assert_array_equal(es, s[m])
+    np.testing.assert_array_equal(ev, v[m])
+    # a window [offset, offset + n) of slots
+    wk, _, _ = t.export_batch_if(kind, pat, th, 2000, offset=3000)
+    k2, _, s2 = t.export_batch(2000, 3000)
+    np.testing.assert_array_equal(wk, k2[_np_pred(kind, k2, s2, pat, th)])
+    assert t.erase_if(kind, pat, th) == int(m.sum())
+    assert t.size() == 3000 - int(m.sum())
+    _, f, _ = t.find(k)
+    np.testing.assert_array_equal(f, ~m)
+    assert t.size_if(kind, pat, th) == 0
+
+
+def test_set_max_capacity_unblocks_growth():
+    t = O.Oracle(1024, 1024, dim=4, strategy=O.CUSTOMIZED)
+    rng = np.random.default_rng(2)
+    with pytest.raises(O.OracleError) as e:
+        t.set_max_capacity(3000)
+    assert e.value.code == 3
+    ks = uniform_keys(rng, 900)
+    t.insert_or_assign(ks, values_for(ks, 4), np.ones(900, np.uint64))
+    assert t.capacity() == 1024
+    t.set_max_capacity(4096)
+    ks2 = uniform_keys(rng, 900, exclude=ks)
+    t.insert_or_assign(ks2, values_for(ks2, 4), np.ones(900, np.uint64))
+    assert t.capacity() == 4096
