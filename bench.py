@@ -491,6 +491,53 @@ def main():
                 "algo_gbs": round(gbs("find_miss", fm_ms), 1)}
             breakdown["find_missed_overload_lf0.5"] = {
                 "mkeys_s": round(BATCH / fmm_ms / 1e3, 1), "ms": round(fmm_ms, 4)}
+            # Pointer, assign and predicate APIs on the same table (load
+            # factor ~0.5, resident keys).
+            hit_keys = find_keys[0]
+            vptrs = torch.empty(BATCH, dtype=torch.int64, device=dev)
+            kptrs = [torch.empty(BATCH, dtype=torch.int64, device=dev) for _ in range(3)]
+            api = {}
+            # One untimed call of each API first (first-launch costs).
+            few = 1024
+            table.find_ptr(few, hit_keys, vptrs, founds, None, stream)
+            table.find_and_update(few, hit_keys, vptrs, founds, None, stream)
+            table.contains(few, hit_keys, founds, stream)
+            table.assign_values(few, hit_keys, values, stream)
+            table.find_or_insert_ptr(few, hit_keys, vptrs, founds, None, stream)
+            cnt = torch.zeros(1, dtype=torch.int64, device=dev)
+            table.size_if(hkv_amd.PRED_SCORE_GE, 0, 0, cnt, stream)
+            win = 1 << 22
+            ek = torch.empty(win, dtype=torch.int64, device=dev)
+            evv = torch.empty((win, DIM), dtype=torch.float32, device=dev)
+            table.export_batch_if(hkv_amd.PRED_SCORE_GE, 0, 0, few, 0, cnt, ek, evv, None,
+                                  stream)
+            torch.cuda.synchronize()
+            api["find_ptr_hit"] = time_op(lambda r: table.find_ptr(
+                BATCH, hit_keys, vptrs, founds, None, stream))
+            api["find_and_update_hit"] = time_op(lambda r: table.find_and_update(
+                BATCH, hit_keys, vptrs, founds, None, stream))
+            api["contains_hit"] = time_op(lambda r: table.contains(
+                BATCH, hit_keys, founds, stream))
+            api["assign_values_hit"] = time_op(lambda r: table.assign_values(
+                BATCH, hit_keys, values, stream))
+            fp_keys = [rand_keys(torch, BATCH, gen) for _ in range(3)]
+            api["find_or_insert_ptr_new"] = time_op(lambda r: table.find_or_insert_ptr(
+                BATCH, fp_keys[r], vptrs, founds, None, stream))
+            api["find_or_insert_ptr_hit_locked"] = time_op(lambda r: table.find_or_insert_ptr(
+                BATCH, fp_keys[r], vptrs, founds, None, stream, True, False, kptrs[r]))
+            api["unlock_keys"] = time_op(lambda r: table.unlock_keys(
+                BATCH, kptrs[r], fp_keys[r], None, stream))
+            api["size_if_full_table"] = time_op(lambda r: table.size_if(
+                hkv_amd.PRED_SCORE_GE, 0, 0, cnt, stream))
+            api["export_batch_if_4M_slots"] = time_op(lambda r: table.export_batch_if(
+                hkv_amd.PRED_SCORE_GE, 0, 0, win, r * win, cnt, ek, evv, None, stream))
+            for name, ms in api.items():
+                per = CAP if name == "size_if_full_table" else (
+                    win if name.startswith("export") else BATCH)
+                breakdown[name] = {"ms": round(ms, 4),
+                                   "mitems_s": round(per / ms / 1e3, 1),
+                                   "items": "slots" if per != BATCH else "keys"}
+            del ek, evv
             for target, name, model in ((0.75, "insert_or_assign_lf0.75", "insert_new"),
                                         (1.0, "insert_or_assign_lf1.0", "insert_evict")):
                 guard = 0

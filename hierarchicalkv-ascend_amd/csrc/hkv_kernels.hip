@@ -3277,6 +3277,7 @@ __global__ __launch_bounds__(kBlock) void k_apply_seq(TableView t, ApplyArgs a, 
   __shared__ uint32_t s_li, s_r1, s_nb;
   const uint32_t tid = threadIdx.x, gl = tid & 15;
   gptr<const u64x2> ent = G(reinterpret_cast<const u64x2*>(ps.ent));
+  int32_t added = 0;  // keys this lane's buckets gained
   for (;;) {
     if (tid == 0) s_li = atomicAdd(&ps.dctr[3], 1u);
     __syncthreads();
@@ -3339,13 +3340,21 @@ __global__ __launch_bounds__(kBlock) void k_apply_seq(TableView t, ApplyArgs a, 
           const uint32_t x = s_srt[o + step];
           apply_key<OP, U>(t, S, a, s_idx[x], s_key[x]);
         }
-        bucket_finish(t, S);
+        // Bucket size now, the live count once per wave at the end.
+        if (gl == 0 && S.bsz != S.bsz0) {
+          G(t.bsize)[S.b] = S.bsz;
+          added += S.bsz - S.bsz0;
+        }
       }
       __syncthreads();
       r0 = r1;
     }
     __syncthreads();  // every thread has read s_li before it is rewritten
   }
+  int64_t w = added;
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) w += shfl_xor_u64((uint64_t)w, m, 64);
+  if ((tid & 63) == 0 && w) atomicAdd(t.live, (unsigned long long)w);
 }
 
 // Slot words -> value and key addresses and founds; with `restore`, the key

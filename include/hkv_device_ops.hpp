@@ -13,7 +13,7 @@
 // templates with its built-in predicates for the C ABI (hkv_erase_if,
 // hkv_size_if, hkv_export_batch_if).
 //
-// One lane per slot.  Functors receive lvalues: `key`, `score` (v1 and
+// One lane per slot at a time.  Functors receive lvalues: `key`, `score` (v1 and
 // size_if: also `pattern`, `threshold`), a `V*` to the slot's row, and the
 // reference's cooperative-group size as 1 (each lane evaluates its own slot).
 #pragma once
@@ -27,9 +27,18 @@ namespace hkv_ops {
 
 constexpr uint64_t kReclaimKey = 0xFFFFFFFFFFFFFFFEull;
 constexpr int kBlock = 256;
+constexpr int kScanUnroll = 4;  // slots per thread per pass of the scanning kernels
 
 __host__ __device__ inline bool is_reserved_word(uint64_t k) {
   return (k & 0xFFFFFFFFFFFFFFFCull) == 0xFFFFFFFFFFFFFFFCull;
+}
+
+// Key (.x) and score (.y) of slot g in one 16-byte load through the global
+// address space: the view holds plain pointers, which the compiler would
+// otherwise access with slower generic (flat) instructions.
+typedef uint64_t slot_pair __attribute__((ext_vector_type(2)));
+__device__ inline slot_pair load_slot(const hkv_device_view& v, uint64_t g) {
+  return ((const __attribute__((address_space(1))) slot_pair*)v.slots)[g];
 }
 
 __device__ inline uint8_t* row_of(const hkv_device_view& v, uint64_t g) {
@@ -38,14 +47,18 @@ __device__ inline uint8_t* row_of(const hkv_device_view& v, uint64_t g) {
   return v.slices[b >> v.slice_shift] + ((b & mask) * v.max_bucket_size + s) * v.row_bytes;
 }
 
-// Wave-aggregated count: one atomic per wave; `live` (optional) takes the
-// negated count.
-__device__ inline void wave_count(bool m, unsigned long long* counter, unsigned long long* live) {
-  const unsigned long long bal = __ballot(m);
-  if ((threadIdx.x & 63) == 0 && bal) {
-    const unsigned long long c = (unsigned long long)__popcll(bal);
-    atomicAdd(counter, c);
-    if (live) atomicAdd(live, 0ull - c);
+// Block-wide sum of per-thread counts, added to *dst by one atomic per
+// block (negated when `negate`).  Every thread of the block calls it.
+__device__ inline void block_add(uint32_t c, uint32_t* s_w, unsigned long long* dst,
+                                 bool negate) {
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) c += __shfl_xor(c, m, 64);
+  if ((threadIdx.x & 63) == 0) s_w[threadIdx.x >> 6] = c;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long t = 0;
+    for (int w = 0; w < kBlock / 64; w++) t += s_w[w];
+    if (t) atomicAdd(dst, negate ? 0ull - t : t);
   }
 }
 
@@ -54,78 +67,160 @@ __device__ inline void wave_count(bool m, unsigned long long* counter, unsigned 
 template <class K, class V, class S, class A>
 __global__ __launch_bounds__(kBlock) void k_erase_if(hkv_device_view v, A a,
                                                      unsigned long long* count) {
-  const uint64_t g = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
-  bool m = false;
-  if (g < v.capacity) {
-    const uint64_t raw = v.slots[2 * g];
-    if (!is_reserved_word(raw)) {
-      K key = (K)raw;
-      S score = (S)v.slots[2 * g + 1];
+  __shared__ uint32_t s_w[kBlock / 64];
+  uint32_t c = 0;
+  const uint64_t stride = (uint64_t)gridDim.x * kBlock;
+  for (uint64_t g0 = (uint64_t)blockIdx.x * kBlock + threadIdx.x; g0 < v.capacity;
+       g0 += kScanUnroll * stride) {
+    uint64_t raw[kScanUnroll], sc[kScanUnroll];
+#pragma unroll
+    for (int q = 0; q < kScanUnroll; q++) {  // independent loads in flight
+      const uint64_t g = g0 + q * stride;
+      slot_pair r;
+      r.x = ~0ull;
+      r.y = 0;
+      if (g < v.capacity) r = load_slot(v, g);
+      raw[q] = r.x;
+      sc[q] = r.y;
+    }
+#pragma unroll
+    for (int q = 0; q < kScanUnroll; q++) {
+      if (is_reserved_word(raw[q])) continue;
+      const uint64_t g = g0 + q * stride;
+      K key = (K)raw[q];
+      S score = (S)sc[q];
       V* value = reinterpret_cast<V*>(row_of(v, g));
-      if (a(key, value, score)) {
-        unsigned long long* kp = reinterpret_cast<unsigned long long*>(v.slots + 2 * g);
-        if (atomicCAS(kp, (unsigned long long)raw, (unsigned long long)kReclaimKey) == raw) {
-          v.slots[2 * g + 1] = 0;
-          v.digests[g] = v.reclaim_digest;
-          atomicSub(v.bucket_sizes + (g >> v.bucket_shift), 1);
-          m = true;
-        }
+      if (!a(key, value, score)) continue;
+      unsigned long long* kp = reinterpret_cast<unsigned long long*>(v.slots + 2 * g);
+      if (atomicCAS(kp, (unsigned long long)raw[q], (unsigned long long)kReclaimKey) ==
+          raw[q]) {
+        v.slots[2 * g + 1] = 0;
+        v.digests[g] = v.reclaim_digest;
+        atomicSub(v.bucket_sizes + (g >> v.bucket_shift), 1);
+        c++;
       }
     }
   }
-  wave_count(m, count, reinterpret_cast<unsigned long long*>(v.live));
+  block_add(c, s_w, count, false);
+  __syncthreads();
+  block_add(c, s_w, reinterpret_cast<unsigned long long*>(v.live), true);
 }
 
 // size_if_kernel: live slots that match.
 template <class K, class V, class S, class A>
 __global__ __launch_bounds__(kBlock) void k_size_if(hkv_device_view v, A a,
                                                     unsigned long long* count) {
-  const uint64_t g = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
-  bool m = false;
-  if (g < v.capacity) {
-    const uint64_t raw = v.slots[2 * g];
-    if (!is_reserved_word(raw)) {
-      K key = (K)raw;
-      S score = (S)v.slots[2 * g + 1];
-      m = a(key, reinterpret_cast<V*>(row_of(v, g)), score);
+  __shared__ uint32_t s_w[kBlock / 64];
+  uint32_t c = 0;
+  const uint64_t stride = (uint64_t)gridDim.x * kBlock;
+  for (uint64_t g0 = (uint64_t)blockIdx.x * kBlock + threadIdx.x; g0 < v.capacity;
+       g0 += kScanUnroll * stride) {
+    uint64_t raw[kScanUnroll], sc[kScanUnroll];
+#pragma unroll
+    for (int q = 0; q < kScanUnroll; q++) {  // independent loads in flight
+      const uint64_t g = g0 + q * stride;
+      slot_pair r;
+      r.x = ~0ull;
+      r.y = 0;
+      if (g < v.capacity) r = load_slot(v, g);
+      raw[q] = r.x;
+      sc[q] = r.y;
+    }
+#pragma unroll
+    for (int q = 0; q < kScanUnroll; q++) {
+      if (is_reserved_word(raw[q])) continue;
+      K key = (K)raw[q];
+      S score = (S)sc[q];
+      if (a(key, reinterpret_cast<V*>(row_of(v, g0 + q * stride)), score)) c++;
     }
   }
-  wave_count(m, count, nullptr);
+  block_add(c, s_w, count, false);
 }
 
 // dump_kernel_if / dump_kernel_if_v2: matching live slots of
-// [offset, offset + n) appended at the device counter (order unspecified).
+// [offset, offset + n).  A block owns kExportPer * kBlock consecutive slots:
+// it evaluates the predicate once per slot, reserves its output range with
+// one atomic, and each wave copies its matched rows cooperatively (one row
+// at a time, lanes across the row).  Order across blocks is unspecified.
+constexpr int kExportPer = 16;
+
 template <class K, class V, class S, class A>
 __global__ __launch_bounds__(kBlock) void k_export_if(hkv_device_view v, A a, uint64_t offset,
                                                       uint64_t n, unsigned long long* counter,
                                                       K* keys, V* values, S* scores) {
-  const uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
-  const uint64_t g = offset + i;
-  bool m = false;
-  K key{};
-  S score{};
-  V* row = nullptr;
-  if (i < n) {
-    const uint64_t raw = v.slots[2 * g];
-    if (!is_reserved_word(raw)) {
-      key = (K)raw;
-      score = (S)v.slots[2 * g + 1];
-      row = reinterpret_cast<V*>(row_of(v, g));
-      m = a(key, row, score);
-    }
+  __shared__ uint32_t s_w[kBlock / 64];
+  __shared__ unsigned long long s_base;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const uint64_t c0 = (uint64_t)blockIdx.x * kBlock * kExportPer;
+  uint32_t mask = 0;
+#pragma unroll
+  for (int j = 0; j < kExportPer; j++) {
+    const uint64_t i = c0 + (uint64_t)j * kBlock + tid;
+    if (i >= n) continue;
+    const uint64_t g = offset + i;
+    const slot_pair r = load_slot(v, g);
+    if (is_reserved_word(r.x)) continue;
+    K key = (K)r.x;
+    S score = (S)r.y;
+    if (a(key, reinterpret_cast<V*>(row_of(v, g)), score)) mask |= 1u << j;
   }
-  const unsigned long long bal = __ballot(m);
-  const uint32_t lane = threadIdx.x & 63;
-  unsigned long long base = 0;
-  if (lane == 0 && bal) base = atomicAdd(counter, (unsigned long long)__popcll(bal));
-  base = __shfl(base, 0, 64);
-  if (m) {
-    const uint64_t pos = base + (uint64_t)__popcll(bal & ((1ull << lane) - 1));
-    keys[pos] = key;
-    if (scores) scores[pos] = score;
-    const uint32_t dim = v.row_bytes / (uint32_t)sizeof(V);
-    V* dst = values + pos * dim;
-    for (uint32_t j = 0; j < dim; j++) dst[j] = row[j];
+  // Exclusive prefix of the per-thread counts over the block.
+  const uint32_t cnt = (uint32_t)__popc(mask);
+  uint32_t x = cnt;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t y = __shfl_up(x, d, 64);
+    if (lane >= (uint32_t)d) x += y;
+  }
+  if (lane == 63) s_w[wv] = x;
+  __syncthreads();
+  uint32_t pre = x - cnt, tot = 0;
+  for (uint32_t q = 0; q < kBlock / 64; q++) {
+    pre += q < wv ? s_w[q] : 0u;
+    tot += s_w[q];
+  }
+  if (tid == 0) s_base = tot ? atomicAdd(counter, (unsigned long long)tot) : 0ull;
+  __syncthreads();
+  uint64_t pos = s_base + pre;
+  const uint32_t dim = v.row_bytes / (uint32_t)sizeof(V);
+#pragma unroll 1
+  for (int j = 0; j < kExportPer; j++) {
+    const bool m = (mask >> j) & 1u;
+    const uint64_t g = offset + c0 + (uint64_t)j * kBlock + tid;
+    uint64_t src = 0;
+    if (m) {
+      const slot_pair r = load_slot(v, g);
+      keys[pos] = (K)r.x;
+      if (scores) scores[pos] = (S)r.y;
+      src = (uint64_t)(uintptr_t)row_of(v, g);
+    }
+    const uint64_t my_pos = pos;
+    pos += m ? 1 : 0;
+    unsigned long long bal = __ballot(m);
+    while (bal) {  // up to four rows per pass: all loads, then all stores
+      int l[4] = {0, 0, 0, 0};
+      int k = 0;
+      for (; k < 4 && bal; k++) {
+        l[k] = __ffsll((long long)bal) - 1;
+        bal &= bal - 1;
+      }
+      const V* sr[4];
+      V* dr[4];
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        sr[q] = reinterpret_cast<const V*>((uintptr_t)__shfl(src, l[q], 64));
+        dr[q] = values + (uint64_t)__shfl(my_pos, l[q], 64) * dim;
+      }
+      for (uint32_t e = lane; e < dim; e += 64) {
+        V t[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+          if (q < k) t[q] = sr[q][e];
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+          if (q < k) dr[q][e] = t[q];
+      }
+    }
   }
 }
 
@@ -190,11 +285,16 @@ inline unsigned blocks_for(uint64_t n) {
 }
 
 // Adds the number of erased slots to *count (device); the caller zeroes it.
+inline unsigned stride_blocks(uint64_t n) {
+  const unsigned b = blocks_for(n);
+  return b < 4096u ? b : 4096u;
+}
+
 template <class K, class V, class S, class A>
 hipError_t erase_if(const hkv_device_view& v, const A& a, unsigned long long* count,
                     hipStream_t s) {
   if (v.capacity == 0) return hipSuccess;
-  hipLaunchKernelGGL((k_erase_if<K, V, S, A>), dim3(blocks_for(v.capacity)), dim3(kBlock), 0,
+  hipLaunchKernelGGL((k_erase_if<K, V, S, A>), dim3(stride_blocks(v.capacity)), dim3(kBlock), 0,
                      s, v, a, count);
   return hipGetLastError();
 }
@@ -205,8 +305,8 @@ hipError_t size_if(const hkv_device_view& v, const A& a, unsigned long long* cou
                    hipStream_t s) {
   hipLaunchKernelGGL(k_zero<unsigned long long>, dim3(1), dim3(1), 0, s, count);
   if (v.capacity)
-    hipLaunchKernelGGL((k_size_if<K, V, S, A>), dim3(blocks_for(v.capacity)), dim3(kBlock), 0,
-                       s, v, a, count);
+    hipLaunchKernelGGL((k_size_if<K, V, S, A>), dim3(stride_blocks(v.capacity)), dim3(kBlock),
+                       0, s, v, a, count);
   return hipGetLastError();
 }
 
@@ -220,8 +320,9 @@ hipError_t export_if(const hkv_device_view& v, const A& a, uint64_t n, uint64_t 
   if (offset >= v.capacity) return hipGetLastError();
   if (n > v.capacity - offset) n = v.capacity - offset;
   if (n == 0) return hipGetLastError();
-  hipLaunchKernelGGL((k_export_if<K, V, S, A>), dim3(blocks_for(n)), dim3(kBlock), 0, s, v, a,
-                     offset, n, counter, keys, values, scores);
+  const uint64_t per = (uint64_t)kBlock * kExportPer;
+  hipLaunchKernelGGL((k_export_if<K, V, S, A>), dim3((unsigned)((n + per - 1) / per)),
+                     dim3(kBlock), 0, s, v, a, offset, n, counter, keys, values, scores);
   return hipGetLastError();
 }
 
