@@ -69,6 +69,18 @@ uint64_t ref_slice_bytes(uint64_t max_slots, uint64_t B, uint64_t row) {
   return std::max(std::max(min_slice, s), 2 * MB);
 }
 
+// Allocation flags of pinned-host value slices.  HKV_HOST_ROWS=coherent or
+// noncoherent selects hipHostMallocCoherent / hipHostMallocNonCoherent; the
+// default is hipHostMallocDefault.  Only kernels of this library touch the
+// rows between calls, and a kernel's completion makes its writes visible
+// either way.
+unsigned host_row_flags() {
+  const char* e = std::getenv("HKV_HOST_ROWS");
+  if (e && std::strcmp(e, "coherent") == 0) return hipHostMallocCoherent;
+  if (e && std::strcmp(e, "noncoherent") == 0) return hipHostMallocNonCoherent;
+  return hipHostMallocDefault;
+}
+
 struct Slice {
   uint8_t* host_ptr;  // non-null for pinned host slices
   uint8_t* dev_ptr;
@@ -181,7 +193,7 @@ struct hkv_table {
         hip_check(hipMalloc(&s.dev_ptr, bytes), "hipMalloc(values)");
         remaining_hbm -= bytes;
       } else {
-        hip_check(hipHostMalloc(&s.host_ptr, bytes, hipHostMallocDefault),
+        hip_check(hipHostMalloc(&s.host_ptr, bytes, host_row_flags()),
                   "hipHostMalloc(values)");
         hip_check(hipHostGetDevicePointer((void**)&s.dev_ptr, s.host_ptr, 0),
                   "hipHostGetDevicePointer");
