@@ -60,6 +60,24 @@ def test_assign_matches_oracle(strategy, dim):
     p.assert_same_state()
 
 
+def test_assign_hybrid_rows():
+    # rows in pinned host slices: assign and assign_values write them in place
+    rng = np.random.default_rng(13)
+    p = _pair(O.LFU, dim=16, max_hbm=(1 << 13) * 64 // 4)
+    assert not p.g.is_pure_hbm_mode()
+    ks = _fill(p, rng)
+    q = np.concatenate([ks[:2500], uniform_keys(rng, 500, exclude=ks)])
+    sc = rng.integers(1, 1 << 30, size=q.size, dtype=np.uint64)
+    rows = rng.standard_normal((q.size, 16)).astype(np.float32)
+    p.o.assign(q, rows, sc)
+    p.g.assign(q.size, to_dev(q), to_dev(rows), to_dev(sc))
+    p.assert_same_state()
+    rows2 = rng.standard_normal((q.size, 16)).astype(np.float32)
+    p.o.assign_values(q, rows2)
+    p.g.assign_values(q.size, to_dev(q), to_dev(rows2))
+    p.assert_same_state()
+
+
 @pytest.mark.parametrize("strategy", [O.LFU, O.CUSTOMIZED])
 def test_assign_repeated_keys(strategy):
     # unique_key=False: scores apply in batch order (exact); for a repeated

@@ -51,6 +51,31 @@ def test_predicates_match_oracle(kind, pat, th, dim):
     p.assert_same_find(ks)
 
 
+def test_predicates_hybrid_rows():
+    # export_batch_if reads rows from pinned host slices; erase_if there
+    import torch
+    rng = np.random.default_rng(77)
+    p = Pair(1 << 13, dim=8, strategy=O.CUSTOMIZED, max_hbm=(1 << 13) * 32 // 4)
+    assert not p.g.is_pure_hbm_mode()
+    ks = uniform_keys(rng, 3000)
+    p.insert_or_assign(ks, values_for(ks, 8), rng.integers(0, 1000, size=ks.size,
+                                                           dtype=np.uint64))
+    cnt = torch.zeros(1, dtype=torch.int64, device="cuda")
+    n = 1 << 13
+    gk = torch.zeros(n, dtype=torch.int64, device="cuda")
+    gv = to_dev(np.zeros((n, 8), np.float32))
+    gs = torch.zeros(n, dtype=torch.int64, device="cuda")
+    p.g.export_batch_if(1, 0, 400, n, 0, cnt, gk, gv, gs)
+    c = int(cnt.item())
+    ok, ov, os_ = p.o.export_batch_if(1, 0, 400, n, 0)
+    assert c == ok.size > 0
+    np.testing.assert_array_equal(
+        _rows(to_np(gk, np.uint64)[:c], to_np(gs, np.uint64)[:c],
+              to_np(gv, np.float32).reshape(-1, 8)[:c]), _rows(ok, os_, ov))
+    assert p.g.erase_if(0, 0, 300) == p.o.erase_if(0, 0, 300)
+    p.assert_same_state()
+
+
 def test_signed_key_predicate():
     import torch
     import hkv_amd as H
