@@ -274,7 +274,51 @@ __device__ __forceinline__ void copy_units(gptr<uint8_t> dst, gptr<const uint8_t
     __builtin_nontemporal_store(c, &d[u + 2 * nl]);
     __builtin_nontemporal_store(e, &d[u + 3 * nl]);
   }
-  for (; u < units; u += nl) __builtin_nontemporal_store(__builtin_nontemporal_load(&s[u]), &d[u]);
+  // At most three units per lane remain: every load is issued before the
+  // first store, so the remainder costs one memory round trip.
+  if (u < units) {
+    const bool o1 = u + nl < units, o2 = u + 2 * nl < units;
+    const T a = __builtin_nontemporal_load(&s[u]);
+    T b{}, c{};
+    if (o1) b = __builtin_nontemporal_load(&s[u + nl]);
+    if (o2) c = __builtin_nontemporal_load(&s[u + 2 * nl]);
+    __builtin_nontemporal_store(a, &d[u]);
+    if (o1) __builtin_nontemporal_store(b, &d[u + nl]);
+    if (o2) __builtin_nontemporal_store(c, &d[u + 2 * nl]);
+  }
+}
+
+// Eviction's two row moves in one pass: the victim's row (at `row`) goes to
+// `out` and the input row takes its place.  Both rows load before any store
+// (`out`, `row` and `in` are distinct rows), four units per lane per round.
+template <int U>
+__device__ __forceinline__ void swap_units(gptr<uint8_t> out, gptr<uint8_t> row,
+                                           gptr<const uint8_t> in, uint32_t bytes, uint32_t r,
+                                           uint32_t nl) {
+  using T = typename UnitT<U>::T;
+  const uint32_t units = bytes / U;
+  gptr<T> o = (gptr<T>)out;
+  gptr<T> w = (gptr<T>)row;
+  gptr<const T> s = (gptr<const T>)in;
+  for (uint32_t u0 = r; u0 < units; u0 += 4 * nl) {
+    T v[4], x[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const uint32_t u = u0 + q * nl;
+      if (u < units) {
+        v[q] = __builtin_nontemporal_load(&w[u]);
+        x[q] = __builtin_nontemporal_load(&s[u]);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const uint32_t u = u0 + q * nl;
+      if (u < units) {
+        __builtin_nontemporal_store(v[q], &o[u]);
+        __builtin_nontemporal_store(x[q], &w[u]);
+      }
+    }
+  }
 }
 
 __device__ __forceinline__ void copy_row(gptr<uint8_t> dst, gptr<const uint8_t> src,

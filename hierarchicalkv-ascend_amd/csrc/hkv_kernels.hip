@@ -452,10 +452,26 @@ __device__ __forceinline__ void accum_units(gptr<uint8_t> dst, gptr<const uint8_
   gptr<V> d = (gptr<V>)dst;
   gptr<const V> s = (gptr<const V>)delta;
   const uint32_t cntv = bytes / sizeof(V);
-  for (uint32_t u = r; u < cntv; u += nl) {
-    V v = s[u];
-    v += d[u];  // `val = delta; val += dst` (accum_or_assign_kernel.h:41-49)
-    d[u] = v;
+  // Four elements per lane per round, every load before the first store
+  // (delta and dst are different rows).
+  for (uint32_t u0 = r; u0 < cntv; u0 += 4 * nl) {
+    V v[4], o[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const uint32_t u = u0 + q * nl;
+      if (u < cntv) {
+        v[q] = s[u];
+        o[q] = d[u];
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const uint32_t u = u0 + q * nl;
+      if (u < cntv) {
+        v[q] += o[q];  // `val = delta; val += dst` (accum_or_assign_kernel.h:41-49)
+        d[u] = v[q];
+      }
+    }
   }
 }
 
@@ -609,18 +625,21 @@ __device__ __forceinline__ void apply_key_in(const TableView& t, Bucket16& S, co
     return;
   }
   gptr<uint8_t> trow = row_ptr(t, S.b, pos);
-  if (OP == OP_INSERT_AND_EVICT && res == R_EVICT) {
+  const bool swapped = OP == OP_INSERT_AND_EVICT && res == R_EVICT;
+  if (swapped) {
     const uint64_t j = ev_slot(a, i, l);
     if (l == 0) {
       G(a.ev_keys)[j] = victim_key;
       if (a.ev_scores) G(a.ev_scores)[j] = victim_score;
     }
-    copy_units<U>(G(a.ev_values) + j * R, trow, R, l, 16);
+    // victim row out and input row in, one pass
+    swap_units<U>(G(a.ev_values) + j * R, trow, in_row, R, l, 16);
   }
   if (res == R_EMPTY || res == R_RECLAIMED) S.bsz++;
 
-  if (OP == OP_FIND_OR_INSERT_PTR) {
-    // No row moves: the caller reads or writes the row through its address.
+  if (OP == OP_FIND_OR_INSERT_PTR || swapped) {
+    // No row moves (the caller goes through the returned address), or both
+    // moves done above.
   } else if (res == R_DUP) {
     if (OP == OP_FIND_OR_INSERT) {
       copy_units<U>(G(a.io_values) + i * (uint64_t)R, trow, R, l, 16);
