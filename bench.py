@@ -467,6 +467,23 @@ def main():
         "load_factor_range": [round(lf_start, 4), round(lf_end, 4)],
     }
 
+    # The same K finds back to back (one event pair): the per-launch rate
+    # without the event split between the step's insert and find.
+    with torch.cuda.stream(stream):
+        fb0 = torch.cuda.Event(enable_timing=True)
+        fb1 = torch.cuda.Event(enable_timing=True)
+        fb0.record(stream)
+        for s in range(K):
+            table.find(BATCH, find_keys[W + s], out_vals, founds, None, stream)
+        fb1.record(stream)
+        torch.cuda.synchronize()
+    fbb_ms = fb0.elapsed_time(fb1) / K
+    fbb_gbs = gbs("find_hit", fbb_ms)
+    breakdown["find_hit_lf0.5_back_to_back"] = {
+        "mkeys_s": round(BATCH / fbb_ms / 1e3, 1), "ms": round(fbb_ms, 4),
+        "algo_gbs": round(fbb_gbs, 1), "frac_hbm": round(fbb_gbs / HBM_PEAK_GBS, 4),
+        "calls": K}
+
     if not args.no_extra:
         with torch.cuda.stream(stream):
             def time_op(fn, reps=3):
