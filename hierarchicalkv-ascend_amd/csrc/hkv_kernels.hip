@@ -2463,6 +2463,8 @@ constexpr uint32_t kFastLds = 704;  // entries of a partition the fast pass take
 constexpr uint8_t kMetaKey = 1;     // new key: key and score written at the slot
 constexpr uint8_t kMetaScore = 2;   // present key: score written
 constexpr uint8_t kMetaMask = 3;
+constexpr uint32_t kSerialKeys = 4;     // keys one serial lane of k_apply_fast applies ...
+constexpr uint32_t kSerialCapFrom = 40;  // ... when its block has more serial buckets
 constexpr uint8_t kTkIn = 1 << 2;   // input row -> table row
 constexpr uint8_t kTkOut = 2 << 2;  // table row -> output row
 constexpr uint8_t kTkAcc = kTkOut;  // accum_or_assign: input delta added into the table row
@@ -3038,7 +3040,17 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
       }
     }
     const uint64_t base = b * (uint64_t)B;
+    // In a block with many serial buckets, a lane takes at most kSerialKeys
+    // keys: the block's time is its longest serial lane, so a long bucket's
+    // rest goes to k_apply_deferred (a 16-lane group with the bucket in
+    // registers), like an evicting one.  Blocks with few serial buckets keep
+    // them whole (the hand-over costs more than it saves there).
+    const uint32_t r_end = s_nser > kSerialCapFrom ? stop + kSerialKeys : c;
     for (uint32_t r = stop; r < c; r++) {
+      if (r >= r_end) {
+        stop = r;
+        break;
+      }
       const uint32_t e = lo + r;
       const uint64_t k = s_key[e];
       const uint64_t i = s_idx[e];
