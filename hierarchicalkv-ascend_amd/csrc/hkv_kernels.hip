@@ -2464,7 +2464,10 @@ constexpr uint8_t kMetaKey = 1;     // new key: key and score written at the slo
 constexpr uint8_t kMetaScore = 2;   // present key: score written
 constexpr uint8_t kMetaMask = 3;
 constexpr uint32_t kSerialKeys = 4;     // keys one serial lane of k_apply_fast applies ...
-constexpr uint32_t kSerialCapFrom = 40;  // ... when its block has more serial buckets
+constexpr uint32_t kSerialCapFrom = 40;  // ... when its block has more serial buckets,
+constexpr uint32_t kSerialLong = 6;      // or (find_or_insert, whose duplicate-heavy
+                                         // batches make long lanes) its bucket has more
+                                         // keys left
 constexpr uint8_t kTkIn = 1 << 2;   // input row -> table row
 constexpr uint8_t kTkOut = 2 << 2;  // table row -> output row
 constexpr uint8_t kTkAcc = kTkOut;  // accum_or_assign: input delta added into the table row
@@ -3045,7 +3048,10 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
     // rest goes to k_apply_deferred (a 16-lane group with the bucket in
     // registers), like an evicting one.  Blocks with few serial buckets keep
     // them whole (the hand-over costs more than it saves there).
-    const uint32_t r_end = s_nser > kSerialCapFrom ? stop + kSerialKeys : c;
+    const uint32_t r_end =
+        (s_nser > kSerialCapFrom || (OP == OP_FIND_OR_INSERT && c - stop > kSerialLong))
+            ? stop + kSerialKeys
+            : c;
     for (uint32_t r = stop; r < c; r++) {
       if (r >= r_end) {
         stop = r;
