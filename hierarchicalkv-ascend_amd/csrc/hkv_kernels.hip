@@ -1680,6 +1680,16 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
           mlast[q] = 0;
         }
         __syncthreads();
+        // The next tile's entries load while this tile's input scores are
+        // gathered (their addresses depend on the entries).
+        u64x2 nq[kHvPer];
+#pragma unroll
+        for (uint32_t r = 0; r < kHvPer; r++) {
+          const uint32_t e = tid + r * kBlock;
+          nq[r].x = kEmptyKey;
+          nq[r].y = 0;
+          if (e < m) nq[r] = ent[base_e + e];
+        }
         for (uint32_t e0 = 0; e0 < m; e0 += kBlock * kHvPer) {
           if (*(volatile uint32_t*)&s_mfull) break;  // block-uniform: set before a barrier
           u64x2 eq[kHvPer];
@@ -1687,10 +1697,18 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
           bool hvq[kHvPer];
 #pragma unroll
           for (uint32_t r = 0; r < kHvPer; r++) {
-            const uint32_t e = e0 + tid + r * kBlock;
-            eq[r].x = kEmptyKey;
-            eq[r].y = 0;
-            if (e < m) eq[r] = ent[base_e + e];
+            eq[r] = nq[r];
+            const uint32_t e = e0 + kBlock * kHvPer + tid + r * kBlock;
+            nq[r].x = kEmptyKey;
+            nq[r].y = 0;
+            if (e < m) nq[r] = ent[base_e + e];
+          }
+          // Input scores of every entry of the tile, issued before the
+          // hashing that tells which entries are heavy.
+#pragma unroll
+          for (uint32_t r = 0; r < kHvPer; r++) {
+            cq[r] = 0;
+            if (sum_in && has_in && e0 + tid + r * kBlock < m) cq[r] = G(a.in_scores)[eq[r].y];
           }
 #pragma unroll
           for (uint32_t r = 0; r < kHvPer; r++) {
@@ -1700,11 +1718,8 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
           }
 #pragma unroll
           for (uint32_t r = 0; r < kHvPer; r++) {
-            cq[r] = 0;
-            if (hvq[r] && sum_in && has_in) {
-              const uint64_t in = G(a.in_scores)[eq[r].y];
-              cq[r] = a.sc.strategy == kLfu ? in : (in & kScoreMask);
-            }
+            const uint64_t in = cq[r];
+            cq[r] = !hvq[r] ? 0 : a.sc.strategy == kLfu ? in : (in & kScoreMask);
           }
           // The wave's leading key (first heavy entry of the tile) is folded
           // over all of the tile's sub-rounds with one reduction.
