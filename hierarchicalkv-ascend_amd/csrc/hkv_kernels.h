@@ -47,15 +47,6 @@ struct ApplyArgs {
   int value_type;  // for accumulation
 };
 
-// Per-call scratch of the route/apply pipeline (owned by the table).
-struct RouteScratch {
-  uint32_t* cnt;     // [buckets] keys routed to each bucket, zero between calls
-  uint32_t* pend;    // [buckets * P] batch indices, arrival order
-  uint32_t* heavy;   // [n / (P+1) + 1] buckets with more than P keys
-  uint32_t* ctrl;    // two 64-byte control blocks (ping-pong)
-  uint32_t P;
-};
-
 // Per-call scratch of the partitioned apply pipeline (owned by the table).
 // A partition is a run of 256 consecutive buckets; the batch is cut into
 // chunks of 1024 keys.  Segment (g, p) = the keys of chunk g that fall in
@@ -75,12 +66,13 @@ struct PartScratch {
   uint32_t* ev_wpre;    // [n / 32 + 1] set bits before each word, within its block of 256 words
   uint32_t* ev_blk;     // [n / 8192 + 3] block offsets, then the record count and records below it
   uint32_t np;          // partitions
+  uint32_t prange;      // partitions per counting pass (LDS histogram size)
   uint32_t chunks;      // batch chunks
   uint32_t cap;         // fixed region size per partition (entries)
 };
 
-// Partitions the pipeline supports (LDS histogram of the counting kernel).
-constexpr uint32_t kMaxPartitions = 16384;
+// Partitions one pass of the counting and scatter kernels holds in LDS.
+constexpr uint32_t kPartRange = 16384;
 constexpr uint32_t kPartBuckets = 256;
 constexpr uint32_t kPartChunk = 1024;
 
@@ -96,8 +88,6 @@ void launch_find_missed(const TableView& t, const uint64_t* keys, uint64_t n,
                         uint64_t* scores, int unit, hipStream_t s);
 void launch_erase(const TableView& t, const uint64_t* keys, uint64_t n,
                   hipStream_t s);
-void launch_apply(const TableView& t, int op, const ApplyArgs& a,
-                  RouteScratch& rs, int parity, hipStream_t s);
 void launch_apply_part(const TableView& t, int op, const ApplyArgs& a,
                        const PartScratch& ps, hipStream_t s);
 // Pointer find_or_insert: placement in batch order, slot words in

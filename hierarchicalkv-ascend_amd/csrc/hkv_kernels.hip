@@ -14,8 +14,8 @@
 //      k_apply_deferred (a 16-lane group per bucket); k_apply_part takes the
 //      partitions it leaves: duplicate-heavy buckets folded per distinct key,
 //      the rest by a lane-per-bucket walk in batch order.
-// The route/apply kernels (per-bucket pending lists) serve tables and batches
-// the partition pipeline does not cover.
+// Tables of any size take this pipeline: one with more partitions than the
+// counting kernels' LDS histogram holds is counted in several passes.
 #include <hip/hip_runtime.h>
 
 #include "hkv_kernels.h"
@@ -343,26 +343,8 @@ __global__ __launch_bounds__(kBlock) void k_erase(TableView t, const uint64_t* _
 }
 
 /* ------------------------------------------------------------------------ */
-/* route + apply (all mutating batch operations)                            */
+/* bucket owner state and per-key apply (all mutating batch operations)    */
 /* ------------------------------------------------------------------------ */
-
-__global__ __launch_bounds__(kBlock) void k_route(TableView t, const uint64_t* __restrict__ keys,
-                                                  uint64_t n, uint32_t* __restrict__ cnt,
-                                                  uint32_t* __restrict__ pend, uint32_t P,
-                                                  uint32_t* __restrict__ heavy,
-                                                  uint32_t* __restrict__ ctrl,
-                                                  uint32_t* __restrict__ ctrl_next) {
-  const uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
-  if (i == 0) ctrl_next[0] = 0;
-  if (i >= n) return;
-  const uint64_t k = keys[i];
-  if (is_reserved(k)) return;
-  const uint64_t gi = global_idx(t, murmur3(k));
-  const uint64_t b = gi >> t.bshift;
-  const uint32_t r = atomicAdd(cnt + b, 1u);
-  if (r < P) pend[b * P + r] = (uint32_t)i;
-  if (r == P) heavy[atomicAdd(ctrl, 1u)] = (uint32_t)b;
-}
 
 enum Outcome : uint32_t { R_DUP = 1, R_EMPTY = 2, R_RECLAIMED = 3, R_EVICT = 4, R_REFUSED = 5 };
 
@@ -712,15 +694,8 @@ __device__ __forceinline__ void bucket_finish(const TableView& t, Bucket16& S) {
   }
 }
 
-// Pending-count word after the lane-per-bucket pass: bits 0-15 hold the
-// number of routed keys, bit 31 marks a bucket handed to the 16-lane pass
-// and bits 16-30 the sorted position it resumes from.
-constexpr uint32_t kDefer = 0x80000000u;
-constexpr uint32_t kLightMax = 16;  // keys per bucket the lane pass holds
-
 // Row tasks queued by a wave of the lane pass, executed cooperatively.  The
 // destination pointer's top bit marks an accumulate task.
-constexpr uint32_t kTaskCap = 256;
 constexpr uint64_t kAccumBit = 1ull << 63;
 
 template <int U, int Q>
@@ -950,214 +925,11 @@ __device__ __forceinline__ bool lane_step(const TableView& t, const ApplyArgs& a
   return true;
 }
 
-// Marks `slot` in the per-lane set of slots whose row is queued for writing;
-// returns whether it was already marked (a second write must flush first so
-// that the later key wins).
-__device__ __forceinline__ bool mark_written(uint32_t& wr0, uint32_t& wr1, uint32_t& wr2,
-                                             uint32_t& wr3, int slot) {
-  const uint32_t bit = 1u << (slot & 31);
-  const uint32_t wq = (uint32_t)slot >> 5;
-  const uint32_t cur = wq == 0 ? wr0 : wq == 1 ? wr1 : wq == 2 ? wr2 : wr3;
-  wr0 |= wq == 0 ? bit : 0u;
-  wr1 |= wq == 1 ? bit : 0u;
-  wr2 |= wq == 2 ? bit : 0u;
-  wr3 |= wq == 3 ? bit : 0u;
-  return (cur & bit) != 0;
-}
-
-// Lane-per-bucket pass: each lane owns one bucket with 1..16 routed keys and
-// applies them in batch order as long as no eviction is needed (the key is
-// present, or an EMPTY slot exists).  At the first key that would evict or be
-// refused the lane stops and hands the rest of the bucket to the 16-lane
-// pass.  Metadata is updated in place by the owning lane; row movements are
-// queued in LDS and executed cooperatively by the wave: at the end for
-// insert_or_assign / insert_and_evict, after every step for operations that
-// read table rows (find_or_insert, accum_or_assign) so that a later key of
-// the same batch sees an earlier key's row.
-template <int OP, int U>
-__global__ __launch_bounds__(kBlock) void k_apply_lpb(TableView t, ApplyArgs a,
-                                                      uint32_t* __restrict__ cnt,
-                                                      const uint32_t* __restrict__ pend,
-                                                      uint32_t P) {
-  __shared__ uint64_t s_src[kBlock / 64][kTaskCap];
-  __shared__ uint64_t s_dst[kBlock / 64][kTaskCap];
-  constexpr bool kStepFlush = OP == OP_FIND_OR_INSERT || OP == OP_ACCUM_OR_ASSIGN;
-  const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const uint64_t b = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
-  const uint32_t B = t.B;
-  const uint32_t R = t.row_bytes;
-  uint32_t c = 0;
-  if (b < t.buckets) c = cnt[b];
-  const bool light = c > 0 && c <= P && c <= kLightMax;
-  uint32_t e[kLightMax];
-#pragma unroll
-  for (uint32_t q = 0; q < kLightMax; q++) e[q] = (light && q < c) ? pend[b * P + q] + 1u : 0u;
-  const uint64_t base = b * (uint64_t)B;
-  int32_t bsz = light ? G(t.bsize)[b] : 0;
-  const int32_t bsz0 = bsz;
-  uint32_t maxc = light ? c : 0;
-#pragma unroll
-  for (int m = 32; m > 0; m >>= 1) {
-    const uint32_t o = __shfl_xor(maxc, m, 64);
-    maxc = o > maxc ? o : maxc;
-  }
-  // Slots whose row is already queued for writing in this call; a second
-  // write to one of them flushes the queue first so that the later key wins.
-  uint32_t wr0 = 0, wr1 = 0, wr2 = 0, wr3 = 0;
-  bool active = light;
-  uint32_t stop = c;
-  uint32_t ntask = 0;
-  const bool has_in = a.in_scores != nullptr;
-  // One-step-ahead prefetch of the next key (batch order).
-  uint32_t m_next = kNone;
-#pragma unroll
-  for (uint32_t q = 0; q < kLightMax; q++)
-    if (e[q] > 0 && e[q] < m_next) m_next = e[q];
-  uint64_t k_next = 0, in_next = 0;
-  if (light) {
-    k_next = G(a.keys)[m_next - 1];
-    if (has_in) in_next = G(a.in_scores)[m_next - 1];
-  }
-  for (uint32_t step = 0; step < maxc; step++) {
-    uint64_t src = 0, dst = 0;
-    bool conflict = false;
-    if (active && step < c) {
-      const uint32_t m = m_next;
-      const uint64_t i = m - 1;
-      const uint64_t k = k_next;
-      const uint64_t in = in_next;
-      m_next = kNone;
-#pragma unroll
-      for (uint32_t q = 0; q < kLightMax; q++)
-        if (e[q] > m && e[q] < m_next) m_next = e[q];
-      if (m_next != kNone) {
-        k_next = G(a.keys)[m_next - 1];
-        if (has_in) in_next = G(a.in_scores)[m_next - 1];
-      }
-      int slot = -1;
-      if (!lane_step<OP>(t, a, b, base, i, k, in, has_in, bsz, src, dst, slot)) {
-        active = false;  // eviction path: hand over from this key on
-        stop = step;
-      } else if (!kStepFlush && dst) {
-        conflict = mark_written(wr0, wr1, wr2, wr3, slot);
-      }
-    }
-    // Queue this step's row tasks; flush first when full or when a slot is
-    // written twice.
-    const uint64_t tm = __ballot(dst != 0);
-    const uint32_t nnew = __popcll(tm);
-    if (kStepFlush || __ballot(conflict) != 0 || ntask + nnew > kTaskCap) {
-      __builtin_amdgcn_wave_barrier();
-      if (ntask) flush_tasks<U, 2>(ntask, s_src[wv], s_dst[wv], R, a.value_type);
-      ntask = 0;
-      if (kStepFlush) __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-      __builtin_amdgcn_wave_barrier();
-    }
-    if (dst) {
-      const uint32_t r = ntask + __popcll(tm & ((1ull << lane) - 1));
-      s_src[wv][r] = src;
-      s_dst[wv][r] = dst;
-    }
-    ntask += nnew;
-    if (kStepFlush) {
-      __builtin_amdgcn_wave_barrier();
-      if (ntask) flush_tasks<U, 2>(ntask, s_src[wv], s_dst[wv], R, a.value_type);
-      ntask = 0;
-      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-      __builtin_amdgcn_wave_barrier();
-    }
-  }
-  __builtin_amdgcn_wave_barrier();
-  if (ntask) flush_tasks<U, 8>(ntask, s_src[wv], s_dst[wv], R, a.value_type);
-  if (light) {
-    if (bsz != bsz0) G(t.bsize)[b] = bsz;
-    cnt[b] = stop == c ? 0u : (kDefer | (stop << 16) | c);
-  }
-  uint32_t added = (uint32_t)(bsz - bsz0);
-#pragma unroll
-  for (int m = 32; m > 0; m >>= 1) added += __shfl_xor(added, m, 64);
-  if (lane == 0 && added) atomicAdd(t.live, (unsigned long long)added);
-}
-
-// One 16-lane group per bucket the lane pass did not finish: buckets with
-// more than 16 (and at most P) routed keys, and buckets handed over at their
-// first eviction.
-template <int OP, int U>
-__global__ __launch_bounds__(kBlock) void k_apply(TableView t, ApplyArgs a,
-                                                  uint32_t* __restrict__ cnt,
-                                                  const uint32_t* __restrict__ pend, uint32_t P) {
-  const uint64_t gid = ((uint64_t)blockIdx.x * kBlock + threadIdx.x) >> 4;
-  const uint32_t l = threadIdx.x & 15;
-  if (gid >= t.buckets) return;
-  const uint32_t raw = cnt[gid];
-  if (raw == 0) return;
-  const uint32_t c = raw & 0xFFFFu;
-  if (c > P) return;
-  const uint32_t first = (raw & kDefer) ? (raw >> 16) & 0x7FFFu : 0u;
-  // Pending indices of this bucket, up to 4 per lane, stored as index + 1.
-  uint32_t e[4];
-#pragma unroll
-  for (int q = 0; q < 4; q++) {
-    const uint32_t s = l + 16 * q;
-    e[q] = s < c ? pend[gid * P + s] + 1u : 0u;
-  }
-  Bucket16 S;
-  bucket_load(t, S, gid, l);
-  uint32_t last = 0;
-  for (uint32_t step = 0; step < c; step++) {
-    uint32_t m = kNone;
-#pragma unroll
-    for (int q = 0; q < 4; q++)
-      if (e[q] > last && e[q] < m) m = e[q];
-    m = group_min_u32(m);
-    last = m;
-    if (step >= first) apply_key<OP, U>(t, S, a, (uint64_t)(m - 1), G(a.keys)[m - 1]);
-  }
-  bucket_finish(t, S);
-  if (l == 0) cnt[gid] = 0;
-}
-
-// Buckets with more than P routed keys: one group per bucket walks the batch
-// in index order.
-template <int OP, int U>
-__global__ __launch_bounds__(kBlock) void k_apply_heavy(TableView t, ApplyArgs a,
-                                                        uint32_t* __restrict__ cnt,
-                                                        const uint32_t* __restrict__ heavy,
-                                                        const uint32_t* __restrict__ ctrl) {
-  const uint32_t nheavy = ctrl[0];
-  const uint64_t groups = ((uint64_t)gridDim.x * kBlock) >> 4;
-  const uint32_t l = threadIdx.x & 15;
-  const uint32_t gslot = (threadIdx.x >> 4) & 3;  // group within the wave
-  for (uint64_t g = ((uint64_t)blockIdx.x * kBlock + threadIdx.x) >> 4; g < nheavy;
-       g += groups) {
-    const uint64_t b = heavy[g];
-    Bucket16 S;
-    bucket_load(t, S, b, l);
-    for (uint64_t base = 0; base < a.n; base += 16) {
-      const uint64_t i = base + l;
-      bool mine = false;
-      uint64_t k = 0;
-      if (i < a.n) {
-        k = G(a.keys)[i];
-        mine = !is_reserved(k) && (global_idx(t, murmur3(k)) >> t.bshift) == b;
-      }
-      uint32_t mask = (uint32_t)(__ballot(mine) >> (16 * gslot)) & 0xFFFFu;
-      while (mask) {
-        const uint32_t q = __builtin_ctz(mask);
-        mask &= mask - 1;
-        apply_key<OP, U>(t, S, a, base + q, shfl_u64(k, (int)q, 16));
-      }
-    }
-    bucket_finish(t, S);
-    if (l == 0) cnt[b] = 0;
-  }
-}
-
 /* ------------------------------------------------------------------------ */
 /* partitioned apply (all mutating batch operations)                         */
 /* ------------------------------------------------------------------------ */
 //
-// 1. k_pcount: per 2048-key chunk g of the batch, the number of keys of each
+// 1. k_pcount: per 1024-key chunk g of the batch, the number of keys of each
 //    partition p (256 consecutive buckets), counted in LDS.
 // 2. k_pscan: per partition, its total and the offset of every segment
 //    (g, p); partitions that fit their fixed region are placed there, larger
@@ -1181,6 +953,23 @@ __device__ __forceinline__ uint64_t bucket_of(const TableView& t, uint64_t k) {
   return global_idx(t, murmur3(k)) >> t.bshift;
 }
 
+// Partition of each of a thread's keys (kNone for reserved keys and keys past
+// the batch).
+__device__ __forceinline__ void chunk_parts(const TableView& t, const uint64_t* __restrict__ keys,
+                                            uint64_t n, uint64_t i0, uint64_t (&kq)[kPartChunk / kBlock],
+                                            uint32_t (&pq)[kPartChunk / kBlock]) {
+#pragma unroll
+  for (uint32_t q = 0; q < kPartChunk / kBlock; q++) {
+    const uint64_t i = i0 + threadIdx.x + q * kBlock;
+    kq[q] = i < n ? keys[i] : kEmptyKey;
+  }
+#pragma unroll
+  for (uint32_t q = 0; q < kPartChunk / kBlock; q++)
+    pq[q] = is_reserved(kq[q]) ? kNone : (uint32_t)(bucket_of(t, kq[q]) / kPartBuckets);
+}
+
+// The LDS histogram holds ps.prange partitions; a table with more partitions
+// is counted in several passes over the chunk's keys, which stay in registers.
 __global__ __launch_bounds__(kBlock) void k_pcount(TableView t, const uint64_t* __restrict__ keys,
                                                    uint64_t n, PartScratch ps) {
   extern __shared__ uint32_t s_h[];
@@ -1188,12 +977,8 @@ __global__ __launch_bounds__(kBlock) void k_pcount(TableView t, const uint64_t* 
   const uint32_t NP = ps.np;
   const uint64_t i0 = (uint64_t)blockIdx.x * kPartChunk;
   uint64_t kq[kPer];
-#pragma unroll
-  for (uint32_t q = 0; q < kPer; q++) {
-    const uint64_t i = i0 + threadIdx.x + q * kBlock;
-    kq[q] = i < n ? keys[i] : kEmptyKey;  // reserved: not counted
-  }
-  for (uint32_t q = threadIdx.x; q < NP; q += kBlock) s_h[q] = 0;
+  uint32_t pq[kPer];
+  chunk_parts(t, keys, n, i0, kq, pq);
   if (blockIdx.x == 0 && threadIdx.x == 0) {
     *ps.spill_top = 0;
     ps.dctr[0] = 0;
@@ -1201,13 +986,18 @@ __global__ __launch_bounds__(kBlock) void k_pcount(TableView t, const uint64_t* 
     ps.dctr[2] = 0;
     ps.dctr[3] = 0;
   }
-  __syncthreads();
-#pragma unroll
-  for (uint32_t q = 0; q < kPer; q++)
-    if (!is_reserved(kq[q])) atomicAdd(&s_h[bucket_of(t, kq[q]) / kPartBuckets], 1u);
-  __syncthreads();
   uint32_t* H = ps.hist + (uint64_t)blockIdx.x * NP;
-  for (uint32_t q = threadIdx.x; q < NP; q += kBlock) H[q] = s_h[q];
+  for (uint32_t p0 = 0; p0 < NP; p0 += ps.prange) {
+    const uint32_t w = NP - p0 < ps.prange ? NP - p0 : ps.prange;
+    for (uint32_t q = threadIdx.x; q < w; q += kBlock) s_h[q] = 0;
+    __syncthreads();
+#pragma unroll
+    for (uint32_t q = 0; q < kPer; q++)
+      if (pq[q] - p0 < w) atomicAdd(&s_h[pq[q] - p0], 1u);  // kNone never falls in range
+    __syncthreads();
+    for (uint32_t q = threadIdx.x; q < w; q += kBlock) H[p0 + q] = s_h[q];
+    __syncthreads();
+  }
 }
 
 // 16 partitions per block of 1024 threads; thread (segment group sg, column
@@ -1279,25 +1069,25 @@ __global__ __launch_bounds__(kBlock) void k_pscatter(TableView t,
   constexpr uint32_t kPer = kPartChunk / kBlock;
   const uint32_t NP = ps.np;
   const uint64_t i0 = (uint64_t)blockIdx.x * kPartChunk;
-  // The chunk's keys and its row of segment offsets load together.
   uint64_t kq[kPer];
-#pragma unroll
-  for (uint32_t q = 0; q < kPer; q++) {
-    const uint64_t i = i0 + threadIdx.x + q * kBlock;
-    kq[q] = i < n ? keys[i] : kEmptyKey;  // reserved: skipped
-  }
+  uint32_t pq[kPer];
+  chunk_parts(t, keys, n, i0, kq, pq);
   const uint32_t* H = ps.hist + (uint64_t)blockIdx.x * NP;
-  for (uint32_t q = threadIdx.x; q < NP; q += kBlock) s_o[q] = H[q];
-  __syncthreads();
   gptr<u64x2> ent = G(reinterpret_cast<u64x2*>(ps.ent));
+  for (uint32_t p0 = 0; p0 < NP; p0 += ps.prange) {
+    const uint32_t w = NP - p0 < ps.prange ? NP - p0 : ps.prange;
+    for (uint32_t q = threadIdx.x; q < w; q += kBlock) s_o[q] = H[p0 + q];
+    __syncthreads();
 #pragma unroll
-  for (uint32_t q = 0; q < kPer; q++) {
-    if (is_reserved(kq[q])) continue;
-    const uint32_t pos = atomicAdd(&s_o[bucket_of(t, kq[q]) / kPartBuckets], 1u);
-    u64x2 v;
-    v.x = kq[q];
-    v.y = i0 + threadIdx.x + q * kBlock;
-    ent[pos] = v;
+    for (uint32_t q = 0; q < kPer; q++) {
+      if (pq[q] - p0 >= w) continue;  // other pass, reserved key or past the batch
+      const uint32_t pos = atomicAdd(&s_o[pq[q] - p0], 1u);
+      u64x2 v;
+      v.x = kq[q];
+      v.y = i0 + threadIdx.x + q * kBlock;
+      ent[pos] = v;
+    }
+    __syncthreads();
   }
 }
 
@@ -1566,8 +1356,7 @@ __device__ __forceinline__ uint64_t heavy_score(const ScoreCtx& c, bool has_in, 
 }
 
 template <int OP, int U>
-__global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a, PartScratch ps,
-                                                         int all) {
+__global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a, PartScratch ps) {
   // accum_or_assign accumulates in place, in batch order, inside this kernel;
   // the other operations record their row movements for k_rowcopy.
   constexpr bool kDeferRows = OP != OP_ACCUM_OR_ASSIGN;
@@ -1608,7 +1397,6 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
                     sizeof(uint32_t) * kPartBuckets * kDgStride,
                 "key map fits the digest rows");
   const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const uint32_t NP = ps.np;
   const uint32_t B = t.B;
   const uint32_t R = t.row_bytes;
   const bool has_in = a.in_scores != nullptr;
@@ -1616,8 +1404,8 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
   gptr<u64x2> ent_w = G(reinterpret_cast<u64x2*>(ps.ent));  // in-place compaction
   gptr<uint64_t> trow = G(ps.trow);
   uint32_t added = 0;
-  // Every partition (accum_or_assign), else the ones k_apply_fast left.
-  const uint32_t nlist = all ? NP : *(volatile uint32_t*)&ps.dctr[2];
+  // The partitions k_apply_fast left.
+  const uint32_t nlist = *(volatile uint32_t*)&ps.dctr[2];
   // Blocks take partitions from a counter, so that a block holding a large
   // partition is not also given a fixed share of the others.
   for (;;) {
@@ -1625,7 +1413,7 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
     __syncthreads();
     const uint32_t li = s_li;
     if (li >= nlist) break;  // block-uniform
-    const uint32_t p = all ? li : ps.plist[li];
+    const uint32_t p = ps.plist[li];
     const uint32_t base_e = ps.pinfo[2 * p], m = ps.pinfo[2 * p + 1];
     const uint64_t part_b0 = (uint64_t)p * kPartBuckets;
     uint32_t m_run = m;  // entries left to the run loop
@@ -3865,64 +3653,23 @@ void launch_erase(const TableView& t, const uint64_t* keys, uint64_t n, hipStrea
 }
 
 template <int OP>
-static void apply_op(const TableView& t, const ApplyArgs& a, RouteScratch& rs, int parity,
-                     hipStream_t s) {
-  uint32_t* ctrl = rs.ctrl + 16 * parity;
-  uint32_t* ctrl_next = rs.ctrl + 16 * (1 - parity);
-  hipLaunchKernelGGL(k_route, dim3(grid_for(a.n, kBlock, 1ull << 31)), dim3(kBlock), 0, s, t,
-                     a.keys, a.n, rs.cnt, rs.pend, rs.P, rs.heavy, ctrl, ctrl_next);
-  const dim3 gl(grid_for(t.buckets, kBlock, 1ull << 31)), bl(kBlock);
-  const dim3 gg(grid_for(t.buckets * 16, kBlock, 1ull << 31));
-  const uint64_t max_heavy = a.n / (rs.P + 1) + 1;
-  const dim3 gh(grid_for(max_heavy * 16, kBlock, 2048));
-  const bool heavy = a.n > rs.P;
-#define HKV_APPLY_U(UU)                                                                  \
-  hipLaunchKernelGGL((k_apply_lpb<OP, UU>), gl, bl, 0, s, t, a, rs.cnt, rs.pend, rs.P);  \
-  hipLaunchKernelGGL((k_apply<OP, UU>), gg, bl, 0, s, t, a, rs.cnt, rs.pend, rs.P);      \
-  if (heavy)                                                                             \
-    hipLaunchKernelGGL((k_apply_heavy<OP, UU>), gh, bl, 0, s, t, a, rs.cnt, rs.heavy, ctrl);
-  switch (a.unit) {
-    case 16: HKV_APPLY_U(16); break;
-    case 8: HKV_APPLY_U(8); break;
-    case 4: HKV_APPLY_U(4); break;
-    case 2: HKV_APPLY_U(2); break;
-    default: HKV_APPLY_U(1); break;
-  }
-#undef HKV_APPLY_U
-}
-
-void launch_apply(const TableView& t, int op, const ApplyArgs& a, RouteScratch& rs, int parity,
-                  hipStream_t s) {
-  switch (op) {
-    case OP_INSERT_OR_ASSIGN: apply_op<OP_INSERT_OR_ASSIGN>(t, a, rs, parity, s); break;
-    case OP_FIND_OR_INSERT: apply_op<OP_FIND_OR_INSERT>(t, a, rs, parity, s); break;
-    case OP_INSERT_AND_EVICT: apply_op<OP_INSERT_AND_EVICT>(t, a, rs, parity, s); break;
-    case OP_ACCUM_OR_ASSIGN: apply_op<OP_ACCUM_OR_ASSIGN>(t, a, rs, parity, s); break;
-    default: apply_op<OP_ASSIGN_SCORES>(t, a, rs, parity, s); break;
-  }
-}
-
-template <int OP>
 static void apply_part_op(const TableView& t, const ApplyArgs& a, const PartScratch& ps,
                           hipStream_t s) {
-  const size_t lds = (size_t)ps.np * sizeof(uint32_t);
+  const size_t lds = (size_t)(ps.np < ps.prange ? ps.np : ps.prange) * sizeof(uint32_t);
   hipLaunchKernelGGL(k_pcount, dim3(ps.chunks), dim3(kBlock), lds, s, t, a.keys, a.n, ps);
   hipLaunchKernelGGL(k_pscan, dim3((ps.np + 15) / 16), dim3(1024), 0, s, ps);
   hipLaunchKernelGGL(k_pscatter, dim3(ps.chunks), dim3(kBlock), lds, s, t, a.keys, a.n, ps);
   const dim3 g(ps.np), b(kBlock);
-  constexpr bool fast = true;
   // After the single-run kernel, the eviction path and the multi-run kernel
   // walk device-side lists that are usually empty: small grids.
   const dim3 gd(grid_for(a.n * 16, kBlock, 2048));
-  const dim3 gp(fast ? (ps.np < 256 ? ps.np : 256) : ps.np);
+  const dim3 gp(ps.np < 256 ? ps.np : 256);
   const uint32_t nw = (uint32_t)((a.n + 31) / 32);
   const uint32_t nbw = (nw + kEvBlkWords - 1) / kEvBlkWords;
 #define HKV_PART_U(UU)                                                                       \
-  if constexpr (fast) {                                                                      \
-    hipLaunchKernelGGL((k_apply_fast<fast ? OP : 0, UU>), g, b, 0, s, t, a, ps);             \
-    hipLaunchKernelGGL((k_apply_deferred<fast ? OP : 0, UU>), gd, b, 0, s, t, a, ps);        \
-  }                                                                                          \
-  hipLaunchKernelGGL((k_apply_part<OP, UU>), gp, b, 0, s, t, a, ps, fast ? 0 : 1);             \
+  hipLaunchKernelGGL((k_apply_fast<OP, UU>), g, b, 0, s, t, a, ps);                          \
+  hipLaunchKernelGGL((k_apply_deferred<OP, UU>), gd, b, 0, s, t, a, ps);                     \
+  hipLaunchKernelGGL((k_apply_part<OP, UU>), gp, b, 0, s, t, a, ps);                         \
   if (OP == OP_FIND_OR_INSERT)                                                               \
     hipLaunchKernelGGL((k_rowtasks<UU>), dim3(grid_for(a.n, kBlock, 2048)), b, 0, s, t, a, ps); \
   if (OP == OP_INSERT_AND_EVICT && a.ev_bits) {                                              \
@@ -3960,7 +3707,7 @@ void launch_find_or_insert_ptr(const TableView& t, const ApplyArgs& a0, const Pa
                                bool keep_locked, hipStream_t s) {
   ApplyArgs a = a0;
   a.slot_out = ps.trow;
-  const size_t lds = (size_t)ps.np * sizeof(uint32_t);
+  const size_t lds = (size_t)(ps.np < ps.prange ? ps.np : ps.prange) * sizeof(uint32_t);
   hipLaunchKernelGGL(k_pcount, dim3(ps.chunks), dim3(kBlock), lds, s, t, a.keys, a.n, ps);
   hipLaunchKernelGGL(k_pscan, dim3((ps.np + 15) / 16), dim3(1024), 0, s, ps);
   hipLaunchKernelGGL(k_pscatter, dim3(ps.chunks), dim3(kBlock), lds, s, t, a.keys, a.n, ps);

@@ -114,16 +114,8 @@ struct hkv_table {
   size_t d_slices_cap = 0;
   bool pure_hbm = true;
 
-  // route/apply scratch
-  uint32_t* cnt = nullptr;
-  uint32_t* pend = nullptr;
-  uint64_t pend_cap = 0;  // entries
-  uint32_t* heavy = nullptr;
-  uint64_t heavy_cap = 0;
-  uint32_t* ctrl = nullptr;
-  int parity = 0;
   // partitioned apply scratch
-  bool force_route = false;  // HKV_APPLY_PATH=route selects the route path
+  uint32_t part_range = kPartRange;  // partitions per counting pass
   uint32_t* p_hist = nullptr;
   uint64_t p_hist_cap = 0;
   uint64_t* p_ent = nullptr;
@@ -181,27 +173,52 @@ struct hkv_table {
     qd_shift = s - 1;
   }
 
-  // Allocates value rows for buckets [b0, b1), HBM while the budget lasts,
-  // then pinned host memory (include/table.h:130-242).
-  void add_slices(uint64_t b0, uint64_t b1) {
-    const uint64_t bps = 1ull << slice_shift;
-    for (uint64_t b = b0; b < b1; b += bps) {
-      const uint64_t nbk = std::min(bps, b1 - b);
-      const uint64_t bytes = std::max<uint64_t>(nbk * B * row, 256);
-      Slice s{nullptr, nullptr, true};
-      if (remaining_hbm >= bytes) {
-        hip_check(hipMalloc(&s.dev_ptr, bytes), "hipMalloc(values)");
-        remaining_hbm -= bytes;
-      } else {
-        hip_check(hipHostMalloc(&s.host_ptr, bytes, host_row_flags()),
-                  "hipHostMalloc(values)");
-        hip_check(hipHostGetDevicePointer((void**)&s.dev_ptr, s.host_ptr, 0),
-                  "hipHostGetDevicePointer");
-        s.hbm = false;
-        pure_hbm = false;
-      }
-      slices.push_back(s);
+  // One slice of `nbk` buckets' rows: HBM while the budget lasts, then
+  // pinned host memory (include/table.h:130-242).
+  Slice alloc_slice(uint64_t nbk) {
+    const uint64_t bytes = std::max<uint64_t>(nbk * B * row, 256);
+    Slice s{nullptr, nullptr, true};
+    if (remaining_hbm >= bytes) {
+      hip_check(hipMalloc(&s.dev_ptr, bytes), "hipMalloc(values)");
+      remaining_hbm -= bytes;
+    } else {
+      hip_check(hipHostMalloc(&s.host_ptr, bytes, host_row_flags()), "hipHostMalloc(values)");
+      hip_check(hipHostGetDevicePointer((void**)&s.dev_ptr, s.host_ptr, 0),
+                "hipHostGetDevicePointer");
+      s.hbm = false;
+      pure_hbm = false;
     }
+    return s;
+  }
+
+  // Allocates value rows for buckets [b0, b1).  Slice j holds buckets
+  // [j << slice_shift, (j + 1) << slice_shift), which is what row_ptr
+  // assumes.  A bucket count that is not a multiple of the slice size leaves
+  // the last slice short; growing past it first replaces that slice with a
+  // longer one and copies its rows over.
+  void add_slices(uint64_t b0, uint64_t b1, hipStream_t st) {
+    const uint64_t bps = 1ull << slice_shift;
+    uint64_t b = b0;
+    if (b0 % bps != 0) {
+      const uint64_t sb0 = b0 - b0 % bps;
+      if (slices.size() != (sb0 >> slice_shift) + 1)
+        fail(HKV_ERR_DEVICE, "value slices out of step with the bucket count");
+      const uint64_t have = b0 - sb0, want = std::min(bps, b1 - sb0);
+      const Slice old = slices.back();
+      // The replacement may take the budget of the slice it replaces.
+      if (old.hbm) remaining_hbm += std::max<uint64_t>(have * B * row, 256);
+      const Slice ns = alloc_slice(want);
+      hip_check(hipMemcpyAsync(ns.dev_ptr, old.dev_ptr, have * B * row, hipMemcpyDefault, st),
+                "hipMemcpyAsync(slice rows)");
+      hip_check(hipStreamSynchronize(st), "hipStreamSynchronize");
+      if (old.hbm) (void)hipFree(old.dev_ptr);
+      else (void)hipHostFree(old.host_ptr);
+      slices.back() = ns;
+      b = sb0 + want;
+    } else if (slices.size() != (b0 >> slice_shift)) {
+      fail(HKV_ERR_DEVICE, "value slices out of step with the bucket count");
+    }
+    for (; b < b1; b += bps) slices.push_back(alloc_slice(std::min(bps, b1 - b)));
     if (slices.size() > d_slices_cap) {
       if (d_slices) hip_check(hipFree(d_slices), "hipFree");
       d_slices_cap = std::max<size_t>(slices.size() * 2, 16);
@@ -225,10 +242,6 @@ struct hkv_table {
     }
     slices.clear();
     (void)hipFree(d_slices);
-    (void)hipFree(cnt);
-    (void)hipFree(pend);
-    (void)hipFree(heavy);
-    (void)hipFree(ctrl);
     (void)hipFree(p_hist);
     (void)hipFree(p_ent);
     (void)hipFree(p_info);
@@ -253,26 +266,12 @@ struct hkv_table {
         .count();
   }
 
-  void ensure_route_scratch(uint64_t n, uint32_t P) {
-    const uint64_t need = nb * P;
-    if (need > pend_cap) {
-      if (pend) hip_check(hipFree(pend), "hipFree");
-      hip_check(hipMalloc(&pend, need * sizeof(uint32_t)), "hipMalloc(pend)");
-      pend_cap = need;
-    }
-    const uint64_t hneed = n / (P + 1) + 1;
-    if (hneed > heavy_cap) {
-      if (heavy) hip_check(hipFree(heavy), "hipFree");
-      hip_check(hipMalloc(&heavy, hneed * sizeof(uint32_t)), "hipMalloc(heavy)");
-      heavy_cap = hneed;
-    }
-  }
-
-  // Scratch of the partitioned apply path for a batch of n keys.  Returns
-  // false when the table has more partitions than the path supports.
-  bool part_scratch(uint64_t n, PartScratch* ps, hipStream_t s) {
+  // Scratch of the partitioned apply path for a batch of n keys.  Entries
+  // are addressed with 32-bit offsets, which bounds a batch below 2^32 keys.
+  void part_scratch(uint64_t n, PartScratch* ps, hipStream_t s) {
     const uint64_t np = (nb + kPartBuckets - 1) / kPartBuckets;
-    if (force_route || np > kMaxPartitions || n >= (1ull << 32)) return false;
+    if (n >= (1ull << 32))
+      fail(HKV_ERR_UNSUPPORTED, "batches of 2^32 keys or more are not supported");
     const uint64_t ng = (n + kPartChunk - 1) / kPartChunk;
     // Fixed region per partition: the mean plus eight standard deviations;
     // a partition that receives more goes to the spill area, which holds n.
@@ -280,6 +279,8 @@ struct hkv_table {
     uint64_t cap = (uint64_t)(mu + 8.0 * std::sqrt(mu) + 64.0);
     cap = (cap + 63) & ~63ull;
     if (np * cap + n >= (1ull << 32)) cap = 64;
+    if (np * cap + n >= (1ull << 32))
+      fail(HKV_ERR_UNSUPPORTED, "batch and table too large for 32-bit entry offsets");
     const uint64_t hist = ng * np, ent = np * cap + n, info = 2 * np;
     if (hist > p_hist_cap) {
       if (p_hist) hip_check(hipFree(p_hist), "hipFree");
@@ -327,20 +328,10 @@ struct hkv_table {
       launch_fill_u32(p_evbits, 0, nw, s);
       p_evw_cap = nw;
     }
-    *ps = PartScratch{p_hist,  p_ent,   p_info,       p_spill,      p_trow,
-                      p_list,  p_drec,  p_dpool,      p_dctr,       p_evbits,
-                      p_evwpre, p_evblk, (uint32_t)np, (uint32_t)ng, (uint32_t)cap};
-    return true;
-  }
-
-  // Pending-list length: large enough that, with keys spread uniformly, a
-  // bucket overflows it with negligible probability.
-  uint32_t pick_P(uint64_t n) const {
-    const double lam = (double)n / (double)nb;
-    if (lam <= 3.0) return 16;
-    if (lam <= 10.0) return 32;
-    if (lam <= 20.0) return 48;
-    return 64;
+    *ps = PartScratch{p_hist,   p_ent,   p_info,       p_spill,    p_trow,
+                      p_list,   p_drec,  p_dpool,      p_dctr,     p_evbits,
+                      p_evwpre, p_evblk, (uint32_t)np, part_range, (uint32_t)ng,
+                      (uint32_t)cap};
   }
 
   uint64_t sampled_size(hipStream_t s) {
@@ -366,27 +357,22 @@ struct hkv_table {
     uint8_t* nd = nullptr;
     uint64_t* nsl = nullptr;
     int32_t* nbs = nullptr;
-    uint32_t* ncnt = nullptr;
     hip_check(hipMalloc(&nd, 2 * old_C), "hipMalloc(digests)");
     hip_check(hipMalloc(&nsl, 2 * old_C * 16), "hipMalloc(slots)");
     hip_check(hipMalloc(&nbs, 2 * old_nb * 4), "hipMalloc(bsize)");
-    hip_check(hipMalloc(&ncnt, 2 * old_nb * 4), "hipMalloc(cnt)");
     hip_check(hipMemcpyAsync(nd, digests, old_C, hipMemcpyDeviceToDevice, s), "copy");
     hip_check(hipMemcpyAsync(nsl, slots, old_C * 16, hipMemcpyDeviceToDevice, s), "copy");
     hip_check(hipMemcpyAsync(nbs, bsize, old_nb * 4, hipMemcpyDeviceToDevice, s), "copy");
-    launch_fill_u32(ncnt, 0, 2 * old_nb, s);
     hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
     (void)hipFree(digests);
     (void)hipFree(slots);
     (void)hipFree(bsize);
-    (void)hipFree(cnt);
     digests = nd;
     slots = nsl;
     bsize = nbs;
-    cnt = ncnt;
     nb = 2 * old_nb;
     set_capacity(2 * old_C);
-    add_slices(old_nb, nb);
+    add_slices(old_nb, nb, s);
     launch_init_slots(view(), old_nb, nb, s);
     launch_rehash(view(), old_nb, value_unit(nullptr), s);
     hip_check(hipGetLastError(), "rehash launch");
@@ -495,16 +481,9 @@ int insert_like(hkv_table* t, int op, uint64_t n, const void* keys, const void* 
   a.unit = min_unit(t, {in_values, io_values, ev_values});
   a.value_type = t->value_type;
   PartScratch ps{};
-  if (t->part_scratch(n, &ps, s)) {
-    if (op == OP_INSERT_AND_EVICT) a.ev_bits = ps.ev_bits;
-    launch_apply_part(t->view(), op, a, ps, s);
-  } else {
-    const uint32_t P = t->pick_P(n);
-    t->ensure_route_scratch(n, P);
-    RouteScratch rs{t->cnt, t->pend, t->heavy, t->ctrl, P};
-    launch_apply(t->view(), op, a, rs, t->parity, s);
-    t->parity ^= 1;
-  }
+  t->part_scratch(n, &ps, s);
+  if (op == OP_INSERT_AND_EVICT) a.ev_bits = ps.ev_bits;
+  launch_apply_part(t->view(), op, a, ps, s);
   hip_check(hipGetLastError(), "kernel launch");
   return HKV_OK;
 }
@@ -566,8 +545,12 @@ int hkv_create(const hkv_options* o, int key_type, int value_type, int strategy,
     t->strategy = strategy;
     t->B = o->max_bucket_size;
     t->row = o->dim * (uint64_t)value_size(value_type);
-    const char* path = std::getenv("HKV_APPLY_PATH");
-    t->force_route = path && std::strcmp(path, "route") == 0;
+    // Test knob: fewer partitions per counting pass, so that small tables
+    // take the multi-pass counting path of very large ones.
+    if (const char* r = std::getenv("HKV_PART_RANGE")) {
+      const long v = std::strtol(r, nullptr, 10);
+      if (v >= 1 && v <= (long)kPartRange) t->part_range = (uint32_t)v;
+    }
     try {
       if (o->device_id >= 0) {
         hip_check(hipSetDevice(o->device_id), "hipSetDevice");
@@ -605,15 +588,11 @@ int hkv_create(const hkv_options* o, int key_type, int value_type, int strategy,
       hip_check(hipMalloc(&t->slots, t->C * 16), "hipMalloc(slots)");
       hip_check(hipMalloc(&t->bsize, t->nb * 4), "hipMalloc(bsize)");
       hip_check(hipMalloc(&t->live, sizeof(uint64_t)), "hipMalloc(live)");
-      hip_check(hipMalloc(&t->cnt, t->nb * 4), "hipMalloc(cnt)");
-      hip_check(hipMalloc(&t->ctrl, 32 * sizeof(uint32_t)), "hipMalloc(ctrl)");
       hip_check(hipMalloc(&t->d_sum, sizeof(uint64_t)), "hipMalloc(sum)");
       hip_check(hipHostMalloc(&t->h_sum, sizeof(uint64_t), hipHostMallocDefault),
                 "hipHostMalloc(sum)");
-      t->add_slices(0, t->nb);
+      t->add_slices(0, t->nb, 0);
       launch_init_slots(t->view(), 0, t->nb, 0);
-      launch_fill_u32(t->cnt, 0, t->nb, 0);
-      launch_fill_u32(t->ctrl, 0, 32, 0);
       launch_fill_u64(t->live, 0, 1, 0);
       hip_check(hipGetLastError(), "init launch");
       hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
@@ -1269,10 +1248,7 @@ int hkv_find_or_insert_ptr(hkv_table* t, uint64_t n, const void* keys, void** va
       fail(HKV_ERR_UNSUPPORTED,
            "unique_key should be true and max_bucket_size should be larger.");
     PartScratch ps{};
-    if (!t->part_scratch(n, &ps, s))
-      fail(HKV_ERR_UNSUPPORTED,
-           "the pointer find_or_insert needs the partitioned apply path "
-           "(at most 2^29 slots, fewer than 2^32 keys per call)");
+    t->part_scratch(n, &ps, s);
     ApplyArgs a{};
     a.keys = reinterpret_cast<const uint64_t*>(keys);
     a.in_scores = scores;

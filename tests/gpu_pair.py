@@ -200,3 +200,91 @@ def records_equal(o, g):
     a = a[np.lexsort(a.T[::-1])] if a.size else a
     b = b[np.lexsort(b.T[::-1])] if b.size else b
     np.testing.assert_array_equal(b, a)
+
+
+class GpuTable:
+    """The gfx950 table (through the C ABI) behind the oracle's numpy-facing
+    method names, so that a known-answer test written against the oracle can
+    run unchanged against the GPU."""
+
+    def __init__(self, init_capacity, max_capacity=None, dim=16,
+                 max_bucket_size=128, strategy=O.LRU, value_type="f32",
+                 max_load_factor=0.5, threads=1):
+        import hkv_amd
+        if max_capacity is None:
+            max_capacity = init_capacity
+        self.torch = _torch()
+        self.dim, self.np_vt = dim, NP_OF[value_type]
+        self.g = hkv_amd.HashTable("u64", value_type, strategy)
+        self.g.init(hkv_amd.HashTableOptions(
+            init_capacity=init_capacity, max_capacity=max_capacity,
+            max_hbm_for_vectors=Pair.BIG_HBM, dim=dim,
+            max_bucket_size=max_bucket_size, max_load_factor=max_load_factor))
+
+    def _v(self, values, n):
+        return np.ascontiguousarray(values, dtype=self.np_vt).reshape(n, self.dim)
+
+    @staticmethod
+    def _s(scores):
+        return None if scores is None else to_dev(np.asarray(scores, np.uint64))
+
+    def set_global_epoch(self, e):
+        self.g.set_global_epoch(e)
+
+    def insert_or_assign(self, keys, values, scores=None, unique_key=True,
+                         ignore_evict_strategy=False, clock=0):
+        keys = np.asarray(keys, np.uint64)
+        self.g.set_lru_clock(clock)
+        self.g.insert_or_assign(keys.size, to_dev(keys), to_dev(self._v(values, keys.size)),
+                                self._s(scores), 0, unique_key, ignore_evict_strategy)
+
+    def find_or_insert(self, keys, values, scores=None, unique_key=True,
+                       ignore_evict_strategy=False, clock=0):
+        keys = np.asarray(keys, np.uint64)
+        v = to_dev(self._v(values, keys.size))
+        self.g.set_lru_clock(clock)
+        self.g.find_or_insert(keys.size, to_dev(keys), v, self._s(scores), 0,
+                              unique_key, ignore_evict_strategy)
+        return to_np(v, self.np_vt).reshape(keys.size, self.dim)
+
+    def accum_or_assign(self, keys, values, accum, scores=None,
+                        ignore_evict_strategy=False, clock=0):
+        keys = np.asarray(keys, np.uint64)
+        self.g.set_lru_clock(clock)
+        self.g.accum_or_assign(keys.size, to_dev(keys), to_dev(self._v(values, keys.size)),
+                               to_dev(np.asarray(accum, np.uint8)), self._s(scores), 0,
+                               ignore_evict_strategy)
+
+    def assign_scores(self, keys, scores=None, clock=0):
+        keys = np.asarray(keys, np.uint64)
+        self.g.set_lru_clock(clock)
+        self.g.assign_scores(keys.size, to_dev(keys), self._s(scores))
+
+    def find(self, keys, values=None, with_scores=False):
+        torch = self.torch
+        keys = np.asarray(keys, np.uint64)
+        n = keys.size
+        if values is None:
+            values = np.zeros((n, self.dim), self.np_vt)
+        v = to_dev(values)
+        f = torch.zeros(n, dtype=torch.uint8, device="cuda")
+        s = torch.zeros(n, dtype=torch.int64, device="cuda") if with_scores else None
+        self.g.find(n, to_dev(keys), v, f, s)
+        return (to_np(v, self.np_vt).reshape(n, self.dim), to_np(f, np.uint8).astype(bool),
+                None if s is None else to_np(s, np.uint64))
+
+    def export_batch(self, n, offset=0):
+        torch = self.torch
+        m = max(1, min(n, self.g.capacity() - offset))
+        k = torch.zeros(m, dtype=torch.int64, device="cuda")
+        v = to_dev(np.zeros((m, self.dim), self.np_vt))
+        s = torch.zeros(m, dtype=torch.int64, device="cuda")
+        c = self.g.export_batch(n, offset, k, v, s)
+        return (to_np(k, np.uint64)[:c], to_np(v, self.np_vt).reshape(m, self.dim)[:c],
+                to_np(s, np.uint64)[:c])
+
+    def size(self):
+        return self.g.size()
+
+    def capacity(self):
+        return self.g.capacity()

@@ -85,11 +85,13 @@ def new_table(strategy, cap, dim, max_cap=None, max_hbm=None):
     return t
 
 
-def export_all(t, dim, chunk=1 << 22, on_device=False):
+def export_all(t, dim, chunk=1 << 22, on_device=False, row_of=None):
     """Keys and scores of the whole table (slot order), in `chunk`-slot
     export_batch calls, as host uint64 arrays (or int64 cuda tensors); also
-    counts exported rows that differ from key_rows(key)."""
+    counts exported rows that differ from row_of(keys) (default key_rows)."""
     torch = _torch()
+    if row_of is None:
+        row_of = lambda k: key_rows(k, dim)  # noqa: E731
     ks = torch.empty(chunk, dtype=torch.int64, device="cuda")
     vs = torch.empty((chunk, dim), dtype=torch.float32, device="cuda")
     ss = torch.empty(chunk, dtype=torch.int64, device="cuda")
@@ -97,7 +99,7 @@ def export_all(t, dim, chunk=1 << 22, on_device=False):
     for off in range(0, t.capacity(), chunk):
         c = t.export_batch(chunk, off, ks, vs, ss)
         if c:
-            bad += int((vs[:c] != key_rows(ks[:c], dim)).any(dim=1).sum().item())
+            bad += int((vs[:c] != row_of(ks[:c])).any(dim=1).sum().item())
             if on_device:
                 out_k.append(ks[:c].clone())
                 out_s.append(ss[:c].clone())
@@ -256,28 +258,43 @@ def test_c3_full_size_zipf_epoch_lfu_properties():
     batches hold about 4e7 distinct keys, so no bucket fills and nothing is
     evicted: then every key seen is stored, with score (epoch of its last
     occurrence << 32) | (its number of occurrences), which is checked for
-    every key; every returned row is its key's."""
+    every key.  Batch b's input row of a key is its key row with column 0 set
+    to b, so the rows that come back tell a copied-out table row (column 0 =
+    the batch of the key's first occurrence) from an input left in place."""
     torch = _torch()
     cap, dim, B = 1 << 27, 32, 1 << 20
     t = new_table(O.EPOCH_LFU, cap, dim)
     rng = np.random.default_rng(204)
     count = np.zeros(1 << 30, np.uint32)
     last = np.zeros(1 << 30, np.uint8)
+    first = torch.full((1 << 30,), 255, dtype=torch.uint8, device="cuda")
     ones = torch.ones(B, dtype=torch.int64, device="cuda")
+
+    def rows_with(kd, col0):
+        r = key_rows(kd, dim)
+        r[:, 0] = col0
+        return r
+
+    copied_out = 0
     for b in range(200):
         e = b // 10
         t.set_global_epoch(e)
         ks = scramble30(zipf_ranks(rng, B, 1.05, 1 << 30))
         kd = dev(ks)
-        v = key_rows(kd, dim)
+        v = rows_with(kd, float(b))
         t.find_or_insert(B, kd, v, ones, 0, False)
-        assert torch.equal(v, key_rows(kd, dim)), b
+        fresh = first[kd] == 255
+        first[kd[fresh]] = b
+        fb = first[kd].to(torch.float32)
+        assert torch.equal(v, rows_with(kd, fb)), b
+        copied_out += int((fb != b).sum().item())
         u, c = np.unique(ks, return_counts=True)
         count[u] += c.astype(np.uint32)
         last[u] = e
+    assert copied_out > 20 * B  # many occurrences hit rows of earlier batches
     seen = np.flatnonzero(count)
     assert t.size() == seen.size
-    ek, es, bad = export_all(t, dim)
+    ek, es, bad = export_all(t, dim, row_of=lambda k: rows_with(k, first[k].to(torch.float32)))
     assert bad == 0
     o = np.argsort(ek)
     assert np.array_equal(ek[o], seen.astype(np.uint64))
@@ -416,7 +433,16 @@ def test_c4_full_size_lfu_properties():
     newk = f.clone()
     newk[:H + 1024] = False
     assert torch.equal(out[newk], deltas[newk])
-    assert bool(f[H + 1024:].float().mean() > 0.5)  # new keys can be evicted by later ones
+    # Only the inserting keys (new, flag clear: batch indices H + 1024 on)
+    # evict, Lfu never refuses them, and a key can only be evicted by a later
+    # key of its bucket: so the last inserting key of every bucket is present.
+    ins = q[H + 1024:]
+    bk = (murmur3_np(ins) & np.uint64(cap - 1)) >> np.uint64(7)
+    _, last_rev = np.unique(bk[::-1], return_index=True)
+    last_ins = ins.size - 1 - last_rev
+    f_ins = f[H + 1024:].cpu().numpy()
+    assert f_ins[last_ins].all()
+    assert int(f_ins.sum()) >= last_ins.size
 
     # assign_scores: found keys gain the input score; absent keys stay absent
     sc0 = torch.empty(q.size, dtype=torch.int64, device="cuda")

@@ -356,6 +356,32 @@ def test_auto_growth_on_insert():
     _check_invariants(t)
 
 
+def test_growth_from_general_capacity():
+    # include/table.h:299-311: init = max = 100,000 gives ceil(100000 / 128) =
+    # 782 buckets; set_max_capacity (include/hkv_hashtable.h:2955-2977) then
+    # lets auto-growth double it once (2 * 200,192 > 2^18).  h mod 2C is
+    # h mod C or h mod C + C, so every key stays or moves to bucket b + 782.
+    rng = np.random.default_rng(12)
+    t = O.Oracle(100_000, 100_000, dim=4, strategy=O.CUSTOMIZED)
+    assert t.capacity() == 782 * 128 and t.bucket_count() == 782
+    ks = uniform_keys(rng, 40_000)
+    t.insert_or_assign(ks, values_for(ks, 4), np.arange(ks.size, dtype=np.uint64))
+    t.set_max_capacity(1 << 18)
+    more = uniform_keys(rng, 60_000, exclude=ks)
+    t.insert_or_assign(more, values_for(more, 4), np.arange(more.size, dtype=np.uint64))
+    assert t.capacity() == 1564 * 128
+    allk = np.concatenate([ks, more])
+    got, f, _ = t.find(allk)
+    assert f.all() and t.size() == allk.size
+    np.testing.assert_array_equal(got, values_for(allk, 4))
+    d, k, s, bsz, v = t.raw()
+    live = (k & np.uint64(0xFFFFFFFFFFFFFFFC)) != np.uint64(0xFFFFFFFFFFFFFFFC)
+    slot = np.flatnonzero(live).astype(np.uint64)
+    home = (murmur3_np(k[live]) % np.uint64(1564 * 128)) // np.uint64(128)
+    np.testing.assert_array_equal(slot // np.uint64(128), home)
+    _check_invariants(t)
+
+
 def _check_invariants(t):
     d, k, s, bsz, v = t.raw()
     B = 128
