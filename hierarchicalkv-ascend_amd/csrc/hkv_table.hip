@@ -9,6 +9,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -86,6 +87,40 @@ struct Slice {
   uint8_t* dev_ptr;
   bool hbm;
 };
+
+}  // namespace
+
+// Partition scratch of hkv_insert_or_assign_noalloc: one file-scope array,
+// a copy per GPU that each GPU holds until the process ends.  On the host
+// the name `scratch` only identifies the symbol; host code uses the device
+// address that hipGetSymbolAddress returned for the GPU (noalloc_base).
+constexpr uint64_t kNoAllocScratchBytes = 64ull << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint8_t* g_scratch_base[kMaxDevices] = {};
+
+// Looks up the scratch array's address on `device`, which must be the
+// current device, once per device.
+void resolve_noalloc_scratch(int device) {
+  if (device < 0 || device >= kMaxDevices) fail(HKV_ERR_DEVICE, "device id out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_base[device]) return;
+  void* p = nullptr;
+  hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+  if (!p) fail(HKV_ERR_DEVICE, "hipGetSymbolAddress(scratch) returned null");
+  g_scratch_base[device] = static_cast<uint8_t*>(p);
+}
+
+uint8_t* noalloc_base(int device) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  uint8_t* p = (device >= 0 && device < kMaxDevices) ? g_scratch_base[device] : nullptr;
+  if (!p) fail(HKV_ERR_DEVICE, "the static scratch array was not resolved on this device");
+  return p;
+}
 
 }  // namespace
 
@@ -266,22 +301,74 @@ struct hkv_table {
         .count();
   }
 
-  // Scratch of the partitioned apply path for a batch of n keys.  Entries
-  // are addressed with 32-bit offsets, which bounds a batch below 2^32 keys.
-  void part_scratch(uint64_t n, PartScratch* ps, hipStream_t s) {
-    const uint64_t np = (nb + kPartBuckets - 1) / kPartBuckets;
+  // The same scratch carved out of the static array instead (no allocation).
+  // Calls on one GPU share the array, so calls that overlap on a GPU race.
+  // The row-task region must start at zero and is cleared with a fill kernel;
+  // the kernels write every other region before they read it.
+  void noalloc_scratch(uint64_t n, PartScratch* ps, hipStream_t s) const {
+    const PartLayout L = part_layout(n);
+    uint8_t* base = noalloc_base(device);
+    uint64_t off = 0;
+    auto take = [&](uint64_t bytes) {
+      uint8_t* p = base + off;
+      off += (bytes + 255) & ~255ull;
+      return p;
+    };
+    auto* trow = reinterpret_cast<uint64_t*>(take(n * 8));
+    auto* hist = reinterpret_cast<uint32_t*>(take(L.hist * 4));
+    auto* ent = reinterpret_cast<uint64_t*>(take(L.ent * 16));
+    auto* info = reinterpret_cast<uint32_t*>(take(L.info * 4));
+    auto* list = reinterpret_cast<uint32_t*>(take(L.np * 4));
+    auto* drec = reinterpret_cast<uint32_t*>(take(n * 16));
+    auto* dpool = reinterpret_cast<uint64_t*>(take(n * 16));
+    auto* dctr = reinterpret_cast<uint32_t*>(take(16));
+    auto* spill = reinterpret_cast<uint32_t*>(take(4));
+    if (off > kNoAllocScratchBytes)
+      fail(HKV_ERR_INVALID,
+           "insert_or_assign_noalloc: this batch needs " + std::to_string(off >> 20) +
+               " MiB of scratch on this table; the static scratch array holds " +
+               std::to_string(kNoAllocScratchBytes >> 20) + " MiB");
+    launch_fill_u64(trow, 0, n, s);
+    *ps = PartScratch{hist,    ent,     info,         spill,      trow,
+                      list,    drec,    dpool,        dctr,       nullptr,
+                      nullptr, nullptr, (uint32_t)L.np, part_range, (uint32_t)L.ng,
+                      (uint32_t)L.cap};
+  }
+
+  // Sizes of the partitioned apply path's scratch for a batch of n keys.
+  // Entries are addressed with 32-bit offsets, which bounds a batch below
+  // 2^32 keys.
+  struct PartLayout {
+    uint64_t np, ng, cap;            // partitions, chunks, fixed region size
+    uint64_t hist, ent, info;        // elements of the histogram, entries, info
+  };
+  PartLayout part_layout(uint64_t n) const {
+    PartLayout L{};
+    L.np = (nb + kPartBuckets - 1) / kPartBuckets;
     if (n >= (1ull << 32))
       fail(HKV_ERR_UNSUPPORTED, "batches of 2^32 keys or more are not supported");
-    const uint64_t ng = (n + kPartChunk - 1) / kPartChunk;
+    L.ng = (n + kPartChunk - 1) / kPartChunk;
     // Fixed region per partition: the mean plus eight standard deviations;
     // a partition that receives more goes to the spill area, which holds n.
-    const double mu = std::ceil((double)n / (double)np);
+    const double mu = std::ceil((double)n / (double)L.np);
     uint64_t cap = (uint64_t)(mu + 8.0 * std::sqrt(mu) + 64.0);
     cap = (cap + 63) & ~63ull;
-    if (np * cap + n >= (1ull << 32)) cap = 64;
-    if (np * cap + n >= (1ull << 32))
+    if (L.np * cap + n >= (1ull << 32)) cap = 64;
+    if (L.np * cap + n >= (1ull << 32))
       fail(HKV_ERR_UNSUPPORTED, "batch and table too large for 32-bit entry offsets");
-    const uint64_t hist = ng * np, ent = np * cap + n, info = 2 * np;
+    L.cap = cap;
+    L.hist = L.ng * L.np;
+    L.ent = L.np * cap + n;
+    L.info = 2 * L.np;
+    return L;
+  }
+
+  // Scratch of the partitioned apply path for a batch of n keys, owned by
+  // the handle and grown on demand.
+  void part_scratch(uint64_t n, PartScratch* ps, hipStream_t s) {
+    const PartLayout L = part_layout(n);
+    const uint64_t np = L.np, ng = L.ng, cap = L.cap;
+    const uint64_t hist = L.hist, ent = L.ent, info = L.info;
     if (hist > p_hist_cap) {
       if (p_hist) hip_check(hipFree(p_hist), "hipFree");
       hip_check(hipMalloc(&p_hist, hist * sizeof(uint32_t)), "hipMalloc(part hist)");
@@ -462,7 +549,7 @@ int min_unit(const hkv_table* t, std::initializer_list<const void*> ps) {
 int insert_like(hkv_table* t, int op, uint64_t n, const void* keys, const void* in_values,
                 void* io_values, const uint64_t* scores, const uint8_t* accum,
                 void* ev_keys, void* ev_values, uint64_t* ev_scores, uint64_t* ev_counter,
-                int strategy, int rule, hipStream_t s) {
+                int strategy, int rule, hipStream_t s, const PartScratch* given = nullptr) {
   ApplyArgs a{};
   a.keys = reinterpret_cast<const uint64_t*>(keys);
   a.in_values = reinterpret_cast<const uint8_t*>(in_values);
@@ -481,7 +568,8 @@ int insert_like(hkv_table* t, int op, uint64_t n, const void* keys, const void* 
   a.unit = min_unit(t, {in_values, io_values, ev_values});
   a.value_type = t->value_type;
   PartScratch ps{};
-  t->part_scratch(n, &ps, s);
+  if (given) ps = *given;
+  else t->part_scratch(n, &ps, s);
   if (op == OP_INSERT_AND_EVICT) a.ev_bits = ps.ev_bits;
   launch_apply_part(t->view(), op, a, ps, s);
   hip_check(hipGetLastError(), "kernel launch");
@@ -591,6 +679,7 @@ int hkv_create(const hkv_options* o, int key_type, int value_type, int strategy,
       hip_check(hipMalloc(&t->d_sum, sizeof(uint64_t)), "hipMalloc(sum)");
       hip_check(hipHostMalloc(&t->h_sum, sizeof(uint64_t), hipHostMallocDefault),
                 "hipHostMalloc(sum)");
+      resolve_noalloc_scratch(t->device);
       t->add_slices(0, t->nb, 0);
       launch_init_slots(t->view(), 0, t->nb, 0);
       launch_fill_u64(t->live, 0, 1, 0);
@@ -629,6 +718,27 @@ int hkv_insert_or_assign(hkv_table* t, uint64_t n, const void* keys, const void*
     insert_like(t, OP_INSERT_OR_ASSIGN, n, keys, values, nullptr, scores, nullptr, nullptr,
                 nullptr, nullptr, nullptr, st, unique_key ? RULE_DIGEST16 : RULE_TILE32,
                 S(stream));
+  });
+}
+
+int hkv_insert_or_assign_noalloc(hkv_table* t, uint64_t n, const void* keys,
+                                 const void* values, const uint64_t* scores, hkv_stream stream,
+                                 int unique_key, int ignore_evict_strategy) {
+  return guarded([&] {
+    need_table(t);
+    const int st = ignore_evict_strategy ? HKV_CUSTOMIZED : t->strategy;
+    if (n == 0) return;
+    if (!keys || !values) fail(HKV_ERR_INVALID, "keys and values must not be null");
+    if (!t->reach_max)
+      fail(HKV_ERR_INVALID,
+           "insert_or_assign_noalloc needs a table at its maximum capacity "
+           "(growing the table allocates)");
+    t->check_scores(st, scores, ignore_evict_strategy != 0);
+    PartScratch ps{};
+    t->noalloc_scratch(n, &ps, S(stream));
+    insert_like(t, OP_INSERT_OR_ASSIGN, n, keys, values, nullptr, scores, nullptr, nullptr,
+                nullptr, nullptr, nullptr, st, unique_key ? RULE_DIGEST16 : RULE_TILE32,
+                S(stream), &ps);
   });
 }
 

@@ -104,6 +104,7 @@ _SIGS = {
     "hkv_create": [_vp, _i32, _i32, _i32, _vp],
     "hkv_destroy": [_vp],
     "hkv_insert_or_assign": [_vp, _u64, _vp, _vp, _vp, _vp, _i32, _i32],
+    "hkv_insert_or_assign_noalloc": [_vp, _u64, _vp, _vp, _vp, _vp, _i32, _i32],
     "hkv_insert_and_evict": [_vp, _u64, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                              _vp, _i32, _i32],
     "hkv_accum_or_assign": [_vp, _u64, _vp, _vp, _vp, _vp, _vp, _i32],
@@ -290,6 +291,17 @@ class HashTable:
                                          _ptr(scores), _stream(stream),
                                          int(unique_key),
                                          int(ignore_evict_strategy)))
+
+    def insert_or_assign_noalloc(self, n, keys, values, scores=None, stream=0,
+                                 unique_key=True, ignore_evict_strategy=False):
+        """insert_or_assign that allocates no device memory (no counterpart
+        in the reference; for callers that cannot allocate).  Needs a table
+        at its maximum capacity and a batch whose scratch fits the library's
+        64 MiB static array; otherwise raises HkvException."""
+        _check(_LIB.hkv_insert_or_assign_noalloc(self._h, n, _ptr(keys), _ptr(values),
+                                                 _ptr(scores), _stream(stream),
+                                                 int(unique_key),
+                                                 int(ignore_evict_strategy)))
 
     def insert_and_evict(self, n, keys, values, scores, evicted_keys,
                          evicted_values, evicted_scores,

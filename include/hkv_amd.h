@@ -127,6 +127,20 @@ int hkv_insert_or_assign(hkv_table* t, uint64_t n, const void* keys,
                          hkv_stream stream, int unique_key,
                          int ignore_evict_strategy);
 
+/* insert_or_assign without any device allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops).  Same arguments and results as
+ * hkv_insert_or_assign; its partition scratch lives in a 64 MiB static
+ * device array (one per GPU, kept until the process ends) instead of
+ * handle-owned buffers.  Fails with HKV_ERR_INVALID, changing nothing, when
+ * the batch needs more than 64 MiB of scratch (batches up to about 6.5e5 keys
+ * fit on a 2^26-slot table) or the table is below its maximum capacity (growth allocates).
+ * All calls on one GPU share the array: calls that overlap on a GPU race. */
+int hkv_insert_or_assign_noalloc(hkv_table* t, uint64_t n, const void* keys,
+                                 const void* values, const uint64_t* scores,
+                                 hkv_stream stream, int unique_key,
+                                 int ignore_evict_strategy);
+
 /* As in the reference, the evicted_* buffers hold n records and
  * `d_evicted_counter` must be 0 at the call: the record count is added to it,
  * and records are written at positions below n before being compacted into
