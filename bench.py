@@ -7,9 +7,10 @@ keys + find of one batch of resident keys (100% hit).  The table is filled
 so that the load factor crosses 0.5 in the middle of the timed steps.
 Inputs are resident in HBM before timing starts.
 
-Prints one JSON line.  Also reported: insert_or_assign at load factors 0.75
-and 1.0, find at 0% hit (plain and missed-keys overload), and the host
-reference (the oracle) timed on a bounded sample of the same workload.
+Prints one JSON line.  Also reported: insert_or_assign and find (100% and
+0% hit, plain and missed-keys overloads) at load factors 0.75 and 1.0, the
+other benchmark configurations, and the host reference (the oracle) timed on
+a bounded sample of the same workload at one thread and at all threads.
 """
 import argparse
 import json
@@ -310,14 +311,44 @@ def run_configs(torch, hkv_amd, stream, gen):
     return out
 
 
-def cpu_baseline(seconds_hint=20.0):
+def cpu_info():
+    """CPU model, physical and logical core counts of this host, and the CPUs
+    this process may run on."""
+    model, cores, phys = None, set(), None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if ":" not in line:
+                    continue
+                k, v = (x.strip() for x in line.split(":", 1))
+                if k == "model name" and model is None:
+                    model = v
+                elif k == "physical id":
+                    phys = v
+                elif k == "core id":
+                    cores.add((phys, v))
+    except OSError:
+        pass
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except AttributeError:
+        allowed = os.cpu_count()
+    return {"cpu_model": model, "physical_cores": len(cores) or None,
+            "logical_cores": os.cpu_count(), "cpus_allowed": allowed}
+
+
+def cpu_baseline(batches=4):
     """The oracle on the host cores: kLru, capacity 2^26, dim 64, filled to
-    load factor ~0.5, then insert_or_assign of new keys and find of resident
-    keys in 2^20-key batches."""
+    load factor ~0.47, then `batches` rounds of insert_or_assign of 2^20 new
+    keys plus find of 2^20 resident keys, at one thread and at all the
+    threads the box gives this process (at most 16).  insert_or_assign is
+    split by bucket range across threads and find by batch range, both with
+    the one-thread results."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
     import oracle as O
-    threads = min(16, os.cpu_count() or 1)
+    info = cpu_info()
+    threads = max(1, min(16, info["cpus_allowed"] or 1))
     t = O.Oracle(CAP, dim=DIM, strategy=O.LRU, threads=threads)
     rng = np.random.default_rng(7)
     resident = []
@@ -329,30 +360,35 @@ def cpu_baseline(seconds_hint=20.0):
         clk += 1
         resident.append(ks)
     resident = np.concatenate(resident)
-    n_ins = n_find = 0
-    t_ins = t_find = 0.0
-    t_start = time.perf_counter()
-    while time.perf_counter() - t_start < seconds_hint and n_ins < 8 * BATCH:
-        ks = rng.integers(0, 2**62, BATCH, dtype=np.uint64)
-        q = rng.choice(resident, BATCH)
-        a = time.perf_counter()
-        t.insert_or_assign(ks, vals, clock=clk)
-        b_ = time.perf_counter()
-        t.find(q)
-        c = time.perf_counter()
-        clk += 1
-        t_ins += b_ - a
-        t_find += c - b_
-        n_ins += BATCH
-        n_find += BATCH
-    val = (n_ins + n_find) / (t_ins + t_find) / 1e6
-    return {"value": round(val, 3), "unit": "Mkeys/s", "cores": threads,
+    out = np.empty((BATCH, DIM), np.float32)
+
+    def run(th):
+        t.set_threads(th)
+        t_ins = t_find = 0.0
+        for _ in range(batches):
+            ks = rng.integers(0, 2**62, BATCH, dtype=np.uint64)
+            q = rng.choice(resident, BATCH)
+            a = time.perf_counter()
+            t.insert_or_assign(ks, vals, clock=clk + _)
+            b_ = time.perf_counter()
+            t.find(q, out)
+            c = time.perf_counter()
+            t_ins += b_ - a
+            t_find += c - b_
+        n = batches * BATCH
+        return (2 * n / (t_ins + t_find) / 1e6, n / t_ins / 1e6, n / t_find / 1e6)
+
+    one = run(1)
+    clk += batches
+    allc = run(threads)
+    return {"value": round(allc[0], 3), "unit": "Mkeys/s", "cores": threads,
             "kind": "port",
-            "sample": ("oracle, kLru cap 2^26 dim 64 at load factor ~0.5: "
-                       f"{n_ins // BATCH} insert_or_assign + {n_find // BATCH} "
-                       "find batches of 2^20 keys, bucket-partitioned threads"),
-            "insert_mkeys_s": round(n_ins / t_ins / 1e6, 3),
-            "find_mkeys_s": round(n_find / t_find / 1e6, 3)}
+            "sample": ("oracle, kLru cap 2^26 dim 64 at load factor ~0.47-0.6: "
+                       f"{batches} insert_or_assign + {batches} find batches of 2^20 keys "
+                       f"at 1 thread, then {batches} + {batches} at {threads} threads"),
+            "insert_mkeys_s": round(allc[1], 3), "find_mkeys_s": round(allc[2], 3),
+            "value_1thread": round(one[0], 3), "insert_mkeys_s_1thread": round(one[1], 3),
+            "find_mkeys_s_1thread": round(one[2], 3), **info}
 
 
 def main():
@@ -575,10 +611,28 @@ def main():
                     "mkeys_s": round(BATCH / t_ms / 1e3, 1), "ms": round(t_ms, 4),
                     "algo_gbs": round(g, 1), "frac_hbm": round(g / HBM_PEAK_GBS, 4),
                     "load_factor_at_start": round(lf0, 4)}
-            hf = time_op(lambda r: table.find(BATCH, nk[r], out_vals, founds,
-                                              None, stream))
-            breakdown["find_hit_lf1.0"] = {"mkeys_s": round(BATCH / hf / 1e3, 1),
-                                           "ms": round(hf, 4)}
+                # find at this load factor: the batches just inserted (hits),
+                # then fresh keys (misses) through both overloads.
+                lf_tag = "lf%.2f" % target if target < 1.0 else "lf1.0"
+                hf = time_op(lambda r: table.find(BATCH, nk[r], out_vals, founds,
+                                                  None, stream))
+                hits = int(founds.sum().item())
+                g = gbs("find_hit", hf)
+                breakdown["find_hit_" + lf_tag] = {
+                    "mkeys_s": round(BATCH / hf / 1e3, 1), "ms": round(hf, 4),
+                    "algo_gbs": round(g, 1), "frac_hbm": round(g / HBM_PEAK_GBS, 4),
+                    "bytes_per_key": algo_bytes("find_hit"), "hits": hits,
+                    "load_factor": round(table.load_factor(stream), 4)}
+                mks = [rand_keys(torch, BATCH, gen) for _ in range(3)]
+                fm = time_op(lambda r: table.find(BATCH, mks[r], out_vals, founds,
+                                                  None, stream))
+                fmm = time_op(lambda r: table.find_missed(
+                    BATCH, mks[r], out_vals, mk, mi, ms_, None, stream))
+                breakdown["find_miss_" + lf_tag] = {
+                    "mkeys_s": round(BATCH / fm / 1e3, 1), "ms": round(fm, 4),
+                    "algo_gbs": round(gbs("find_miss", fm), 1),
+                    "missed_overload_ms": round(fmm, 4),
+                    "missed_overload_mkeys_s": round(BATCH / fmm / 1e3, 1)}
 
     if not args.no_configs:
         breakdown.update(run_configs(torch, hkv_amd, stream, gen))

@@ -53,79 +53,6 @@ __global__ void k_init_slots(TableView t, uint64_t s0, uint64_t s1, uint64_t b0,
 /* find                                                                      */
 /* ------------------------------------------------------------------------ */
 
-// find_without_lock (include/find_utils.h:31-86): 4-slot groups from
-// align4(start) with wrap; in each group a slot holding the key is a hit, and
-// otherwise an EMPTY slot ends the search (in the first group only at or
-// after `start`).  The search visits B/4 + 1 groups, the first one twice.
-//
-// Two equivalent ways to test a group: compare the digests (one 16-byte load
-// covers four groups) and confirm matches with the key, or compare the four
-// keys of the group directly.  With `key_first` the groups that lie in
-// start's 128-byte line of slot records are tested by key (at load factors
-// well below 1 the search nearly always ends there, saving the digest line);
-// the rest of the search uses digests.  A slot's digest is the empty digest
-// exactly when its key is EMPTY, so both tests give the same answer.
-//
-// probe_find_from continues a search at group offset `off` (a multiple of 4).
-__device__ __forceinline__ int probe_find_from(const TableView& t, uint64_t b, uint32_t start,
-                                               uint32_t d, uint64_t k, bool key_first,
-                                               uint32_t off) {
-  const uint32_t B = t.B;
-  const uint64_t base = b * B;
-  const uint32_t a = start & ~3u;
-  if (key_first) {
-    // Groups a and, when a opens a line of 8 records, a + 4.
-    const uint32_t line_end = (a & 4u) ? 4u : 8u;
-    for (; off < line_end; off += 4) {
-      const uint32_t g = a + off;
-      uint32_t hit = kNone, empty = kNone;
-#pragma unroll
-      for (uint32_t j = 0; j < 4; j++) {
-        const uint64_t kj = slot_key(t, base + g + j);
-        if (kj == k && hit == kNone) hit = j;
-        if (kj == kEmptyKey && empty == kNone && (off != 0 || g + j >= start)) empty = j;
-      }
-      if (hit != kNone) return (int)(g + hit);
-      if (empty != kNone) return -1;
-    }
-  }
-  gptr<const uint8_t> dg = digest_row(t, b);
-  const uint32_t rep = d * 0x01010101u;
-  const uint32_t erep = (uint32_t)kEmptyDigest * 0x01010101u;
-  uint32_t cur = kNone;
-  u32x4 chunk = {0, 0, 0, 0};
-  for (; off < B + 4; off += 4) {
-    const uint32_t g = (a + off) & (B - 1);
-    const uint32_t c = g >> 4;
-    if (c != cur) {
-      chunk = *(gptr<const u32x4>)(dg + (c << 4));
-      cur = c;
-    }
-    const uint32_t wi = (g >> 2) & 3;
-    const uint32_t w = wi == 0 ? chunk.x : wi == 1 ? chunk.y : wi == 2 ? chunk.z : chunk.w;
-    uint32_t m = eq_bytes4(w, rep);
-    while (m) {
-      const uint32_t j = __builtin_ctz(m);
-      m &= m - 1;
-      if (slot_key(t, base + g + j) == k) return (int)(g + j);
-    }
-    uint32_t e = eq_bytes4(w, erep);
-    while (e) {
-      const uint32_t j = __builtin_ctz(e);
-      e &= e - 1;
-      const uint32_t p = g + j;
-      if (off == 0 && p < start) continue;
-      return -1;  // the empty digest marks an EMPTY slot
-    }
-  }
-  return -1;
-}
-
-__device__ __forceinline__ int probe_find(const TableView& t, uint64_t b, uint32_t start,
-                                          uint32_t d, uint64_t k, bool key_first) {
-  return probe_find_from(t, b, start, d, k, key_first, 0);
-}
-
 // Key-first probing pays off while the table is at most 3/4 full.
 __device__ __forceinline__ bool use_key_first(const TableView& t) {
   return *G(t.live) * 4 < t.capacity * 3;
@@ -175,14 +102,6 @@ __device__ __forceinline__ void wave_copy_rows(uint32_t rows, const uint32_t* ld
   }
 }
 
-// First step of a key-first search: load the four keys of the key's first
-// group.  find_tail recomputes the hash and completes the search.
-struct FindHead {
-  uint64_t k;
-  uint64_t g0, g1, g2, g3;
-  bool valid;
-};
-
 struct KeyPos {
   uint64_t b;
   uint32_t start, d;
@@ -194,43 +113,172 @@ __device__ __forceinline__ KeyPos key_pos(const TableView& t, uint64_t k) {
   return KeyPos{gi >> t.bshift, (uint32_t)(gi & (t.B - 1)), key_digest(h)};
 }
 
-__device__ __forceinline__ void find_head(const TableView& t, FindHead& f, uint64_t k,
-                                          bool valid, bool kf) {
-  f.k = k;
-  f.valid = valid && !is_reserved(k);
-  f.g0 = f.g1 = f.g2 = f.g3 = 0;
-  if (f.valid && kf) {
-    const KeyPos q = key_pos(t, k);
-    gptr<const uint64_t> rec = G(t.slots) + 2 * (q.b * t.B + (q.start & ~3u));
-    f.g0 = rec[0];
-    f.g1 = rec[2];
-    f.g2 = rec[4];
-    f.g3 = rec[6];
+constexpr uint64_t kLocMask = (1ull << 56) - 1;
+
+// Per-wave LDS of wave_probe.
+struct ProbeLds {
+  uint64_t key[64];
+  uint64_t loc[64];    // digest << 56 | (b * B + start) of the lane's key; ~0 when none
+  uint32_t dm[64][8];  // per listed key and 16-slot chunk: match bits | EMPTY bits << 16
+  uint32_t list[64];   // lanes whose keys the digest pass probes
+};
+
+// 128-bit mask (lo, hi) rotated right by r < 128: bit i becomes bit i - r.
+__device__ __forceinline__ void rot128(uint64_t& lo, uint64_t& hi, uint32_t r) {
+  if (r & 64) {
+    const uint64_t x = lo;
+    lo = hi;
+    hi = x;
+  }
+  r &= 63;
+  if (r) {
+    const uint64_t l = (lo >> r) | (hi << (64 - r));
+    const uint64_t h = (hi >> r) | (lo << (64 - r));
+    lo = l;
+    hi = h;
   }
 }
 
-// Slot of the key (bucket in *b), or -1.
-__device__ __forceinline__ int find_tail(const TableView& t, const FindHead& f, bool kf,
-                                         uint64_t* b) {
-  if (!f.valid) return -1;
-  const KeyPos q = key_pos(t, f.k);
-  *b = q.b;
-  if (!kf) return probe_find(t, q.b, q.start, q.d, f.k, false);
-  const uint32_t a = q.start & ~3u;
-  if (f.g0 == f.k) return (int)a;
-  if (f.g1 == f.k) return (int)a + 1;
-  if (f.g2 == f.k) return (int)a + 2;
-  if (f.g3 == f.k) return (int)a + 3;
-  const uint32_t r = q.start - a;  // EMPTY slots before start do not end the search
-  if ((f.g0 == kEmptyKey && r == 0) || (f.g1 == kEmptyKey && r <= 1) ||
-      (f.g2 == kEmptyKey && r <= 2) || f.g3 == kEmptyKey)
-    return -1;
-  return probe_find_from(t, q.b, q.start, q.d, f.k, true, 4);
+// Wave-cooperative lookup of one key per lane (find_without_lock,
+// include/find_utils.h:31-86); returns the slot of the lane's key (bucket in
+// *bk) or -1.  Buckets hold 128 slots.
+//  1. Key-first (kf, the table at most 3/4 full): in each of four loads,
+//     lanes 4q..4q+3 read the keys of the first probe group of key q (one
+//     64-byte request per key); two ballots give every key the group's hit
+//     and EMPTY slots.  The group decides when it holds the key or an EMPTY
+//     slot at or after start.
+//  2. The other keys: lanes 8q..8q+7 read the eight 16-byte chunks of key
+//     q's digest line (one 128-byte request per key) and leave match and
+//     EMPTY masks in LDS.  The owner lane rotates them into probe order from
+//     align4(start), cuts them after the group of the first EMPTY slot (in
+//     the first group only at or after start), and confirms the digest
+//     matches in that order with key loads.  This visits slots in the order
+//     of the reference's group loop and stops where it stops.
+// A slot's digest is the empty digest exactly when its key is EMPTY.
+__device__ __forceinline__ int wave_probe(const TableView& t, uint64_t k, bool valid, bool kf,
+                                          ProbeLds& L, uint64_t* bk) {
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t B = t.B;
+  uint64_t b = 0;
+  uint32_t start = 0, d = 0;
+  if (valid) {
+    const KeyPos q = key_pos(t, k);
+    b = q.b;
+    start = q.start;
+    d = q.d;
+  }
+  *bk = b;
+  L.key[lane] = k;
+  L.loc[lane] = valid ? ((uint64_t)d << 56) | (b * B + start) : ~0ull;
+  __builtin_amdgcn_wave_barrier();
+  int slot = -1;
+  bool done = !valid;
+  if (kf) {
+    uint64_t hit[4], emp[4];
+#pragma unroll
+    for (uint32_t j = 0; j < 4; j++) {
+      const uint32_t o = j * 16 + (lane >> 2);
+      const uint64_t raw = L.loc[o];
+      const uint64_t ok = L.key[o];
+      const bool live = raw != ~0ull;
+      const uint64_t loc = raw & kLocMask;
+      const uint32_t pos = lane & 3;
+      uint64_t kk = 0;
+      if (live) kk = slot_key(t, (loc & ~3ull) + pos);
+      hit[j] = __ballot(live && kk == ok);
+      emp[j] = __ballot(live && kk == kEmptyKey && pos >= (uint32_t)(loc & 3));
+    }
+    const uint32_t j = lane >> 4, sh = 4 * (lane & 15);
+    const uint64_t H = j == 0 ? hit[0] : j == 1 ? hit[1] : j == 2 ? hit[2] : hit[3];
+    const uint64_t E = j == 0 ? emp[0] : j == 1 ? emp[1] : j == 2 ? emp[2] : emp[3];
+    const uint32_t h4 = (uint32_t)(H >> sh) & 15u, e4 = (uint32_t)(E >> sh) & 15u;
+    if (!done && h4) {
+      slot = (int)((start & ~3u) + __builtin_ctz(h4));
+      done = true;
+    } else if (!done && e4) {
+      done = true;
+    }
+  }
+  const uint64_t pend = __ballot(!done);
+  const uint32_t cnt = __popcll(pend);
+  if (cnt == 0) return slot;
+  const uint32_t my = __popcll(pend & ((1ull << lane) - 1));
+  if (!done) L.list[my] = lane;
+  __builtin_amdgcn_wave_barrier();
+  {
+    const uint32_t c = lane & 7;
+    u32x4 w[8];
+#pragma unroll
+    for (uint32_t r = 0; r < 8; r++) {
+      const uint32_t idx = r * 8 + (lane >> 3);
+      w[r] = u32x4{0, 0, 0, 0};
+      if (idx < cnt) {
+        const uint64_t loc = L.loc[L.list[idx]] & kLocMask;
+        w[r] = *(gptr<const u32x4>)(G(t.digests) + (loc & ~(uint64_t)(B - 1)) + c * 16);
+      }
+    }
+    const uint32_t erep = (uint32_t)kEmptyDigest * 0x01010101u;
+#pragma unroll
+    for (uint32_t r = 0; r < 8; r++) {
+      const uint32_t idx = r * 8 + (lane >> 3);
+      if (idx < cnt) {
+        const uint32_t rep = (uint32_t)(L.loc[L.list[idx]] >> 56) * 0x01010101u;
+        const uint32_t m = eq_bytes4(w[r].x, rep) | (eq_bytes4(w[r].y, rep) << 4) |
+                           (eq_bytes4(w[r].z, rep) << 8) | (eq_bytes4(w[r].w, rep) << 12);
+        const uint32_t e = eq_bytes4(w[r].x, erep) | (eq_bytes4(w[r].y, erep) << 4) |
+                           (eq_bytes4(w[r].z, erep) << 8) | (eq_bytes4(w[r].w, erep) << 12);
+        L.dm[idx][c] = m | (e << 16);
+      }
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  if (done) return slot;
+  uint64_t mlo = 0, mhi = 0, elo = 0, ehi = 0;
+#pragma unroll
+  for (uint32_t c = 0; c < 8; c++) {
+    const uint32_t v = L.dm[my][c];
+    const uint64_t m = v & 0xFFFFu, e = v >> 16;
+    if (c < 4) {
+      mlo |= m << (16 * c);
+      elo |= e << (16 * c);
+    } else {
+      mhi |= m << (16 * (c - 4));
+      ehi |= e << (16 * (c - 4));
+    }
+  }
+  const uint32_t a = start & ~3u;
+  rot128(mlo, mhi, a);
+  rot128(elo, ehi, a);
+  elo &= ~((1ull << (start - a)) - 1);  // first group: EMPTY only at or after start
+  if (kf) mlo &= ~0xFull;               // the first group was read by key
+  // Keep the matches up to the end of the first EMPTY slot's group.
+  if (elo) {
+    const uint32_t lim = ((__builtin_ctzll(elo) >> 2) + 1) * 4;
+    mlo &= lim >= 64 ? ~0ull : ((1ull << lim) - 1);
+    mhi = 0;
+  } else if (ehi) {
+    const uint32_t lim = ((__builtin_ctzll(ehi) >> 2) + 1) * 4;
+    mhi &= lim >= 64 ? ~0ull : ((1ull << lim) - 1);
+  }
+  const uint64_t base = b * B;
+  while (mlo | mhi) {
+    uint32_t i;
+    if (mlo) {
+      i = __builtin_ctzll(mlo);
+      mlo &= mlo - 1;
+    } else {
+      i = 64 + __builtin_ctzll(mhi);
+      mhi &= mhi - 1;
+    }
+    const uint32_t p = (a + i) & (B - 1);
+    if (slot_key(t, base + p) == k) return (int)p;
+  }
+  return -1;
 }
 
-// One key per lane; the wave copies its hit rows.  Find is bound by HBM
-// traffic (a 128-byte metadata line plus the row in and out per hit), so more
-// work per wave does not help.  The missed-keys variant runs 1024-thread
+// One key per lane, probed by the wave together (wave_probe); the wave then
+// copies its hit rows.  Find is bound by HBM traffic (a metadata line plus
+// the row in and out per hit).  The missed-keys variant runs 1024-thread
 // blocks and appends a block's missed keys, collected in LDS, with one
 // atomic.
 template <int U, bool MISSED, int BLK>
@@ -243,6 +291,7 @@ __global__ __launch_bounds__(BLK) void k_find(TableView t, const uint64_t* __res
                                               int32_t* __restrict__ missed_size) {
   constexpr uint32_t kMissCap = MISSED ? BLK : 1;
   __shared__ uint32_t s_rows[BLK / 64][64];
+  __shared__ ProbeLds s_probe[BLK / 64];
   __shared__ uint64_t s_mkey[kMissCap];
   __shared__ uint32_t s_midx[kMissCap];
   __shared__ uint32_t s_mcnt, s_mbase;
@@ -251,34 +300,29 @@ __global__ __launch_bounds__(BLK) void k_find(TableView t, const uint64_t* __res
   const bool kf = use_key_first(t);
   if (MISSED && threadIdx.x == 0) s_mcnt = 0;
   if (MISSED) __syncthreads();
-  const uint64_t base0 = ((uint64_t)blockIdx.x * (BLK / 64) + wv) * 64;
-  const uint64_t i0 = base0 + lane;
-  FindHead f0;
-  find_head(t, f0, i0 < n ? keys[i0] : 0, i0 < n, kf);
-  auto finish = [&](const FindHead& f, uint64_t wave_base) __attribute__((always_inline)) {
-    const uint64_t i = wave_base + lane;
-    uint64_t b = 0;
-    const int p = find_tail(t, f, kf, &b);
-    const bool found = p >= 0;
-    gptr<const uint8_t> src = nullptr;
-    if (found) {
-      src = row_ptr(t, b, (uint32_t)p);
-      if (scores) scores[i] = slot_score(t, b * t.B + p);
-    }
-    if (!MISSED && founds && i < n) founds[i] = found ? 1 : 0;
-    if (MISSED && i < n && !found) {
-      const uint32_t r = atomicAdd(&s_mcnt, 1u);
-      s_mkey[r] = f.k;
-      s_midx[r] = (uint32_t)i;
-    }
-    const uint64_t hm = __ballot(found);
-    if (found) s_rows[wv][__popcll(hm & ((1ull << lane) - 1))] = lane;
-    __builtin_amdgcn_wave_barrier();
-    const uint32_t rows = __popcll(hm);
-    if (rows) wave_copy_rows<U>(rows, s_rows[wv], src, values, wave_base, t.row_bytes);
-    __builtin_amdgcn_wave_barrier();
-  };
-  finish(f0, base0);
+  const uint64_t wave_base = ((uint64_t)blockIdx.x * (BLK / 64) + wv) * 64;
+  const uint64_t i = wave_base + lane;
+  const uint64_t k = i < n ? keys[i] : 0;
+  const bool valid = i < n && !is_reserved(k);
+  uint64_t b = 0;
+  const int p = wave_probe(t, k, valid, kf, s_probe[wv], &b);
+  const bool found = p >= 0;
+  gptr<const uint8_t> src = nullptr;
+  if (found) {
+    src = row_ptr(t, b, (uint32_t)p);
+    if (scores) scores[i] = slot_score(t, b * t.B + p);
+  }
+  if (!MISSED && founds && i < n) founds[i] = found ? 1 : 0;
+  if (MISSED && i < n && !found) {
+    const uint32_t r = atomicAdd(&s_mcnt, 1u);
+    s_mkey[r] = k;
+    s_midx[r] = (uint32_t)i;
+  }
+  const uint64_t hm = __ballot(found);
+  if (found) s_rows[wv][__popcll(hm & ((1ull << lane) - 1))] = lane;
+  __builtin_amdgcn_wave_barrier();
+  const uint32_t rows = __popcll(hm);
+  if (rows) wave_copy_rows<U>(rows, s_rows[wv], src, values, wave_base, t.row_bytes);
   if (MISSED) {
     __syncthreads();
     const uint32_t cnt = s_mcnt;
@@ -3231,21 +3275,19 @@ __global__ __launch_bounds__(kBlock) void k_find_ptr(TableView t, const uint64_t
                                                      uint64_t n, uint64_t* __restrict__ vptrs,
                                                      uint8_t* __restrict__ founds,
                                                      uint64_t* __restrict__ scores, ScoreCtx sc) {
+  __shared__ ProbeLds s_probe[kBlock / 64];
   const uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
+  const uint64_t k = i < n ? keys[i] : 0;
+  uint64_t b = 0;
+  const int p = wave_probe(t, k, i < n && !is_reserved(k), use_key_first(t),
+                           s_probe[threadIdx.x >> 6], &b);
   if (i >= n) return;
-  const uint64_t k = keys[i];
-  int p = -1;
-  KeyPos q{};
-  if (!is_reserved(k)) {
-    q = key_pos(t, k);
-    p = probe_find(t, q.b, q.start, q.d, k, false);
-  }
   if (p < 0) {
     vptrs[i] = 0;
     if (founds) founds[i] = 0;
     return;
   }
-  const uint64_t g = q.b * t.B + (uint32_t)p;
+  const uint64_t g = b * t.B + (uint32_t)p;
   if (UPDATE) {
     const bool has_in = scores != nullptr;
     const uint64_t in = has_in ? scores[i] : 0;
@@ -3257,7 +3299,7 @@ __global__ __launch_bounds__(kBlock) void k_find_ptr(TableView t, const uint64_t
   } else if (scores) {
     scores[i] = slot_score(t, g);
   }
-  vptrs[i] = (uint64_t)(uintptr_t)row_ptr(t, q.b, (uint32_t)p);
+  vptrs[i] = (uint64_t)(uintptr_t)row_ptr(t, b, (uint32_t)p);
   if (founds) founds[i] = 1;
 }
 
@@ -3269,26 +3311,26 @@ __global__ __launch_bounds__(kBlock) void k_lock_keys(TableView t, const uint64_
                                                       uint8_t* __restrict__ success,
                                                       const uint64_t* __restrict__ scores,
                                                       ScoreCtx sc) {
+  __shared__ ProbeLds s_probe[kBlock / 64];
   const uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
+  const uint64_t k = i < n ? keys[i] : 0;
+  uint64_t b = 0;
+  const int p = wave_probe(t, k, i < n && !is_reserved(k), use_key_first(t),
+                           s_probe[threadIdx.x >> 6], &b);
   if (i >= n) return;
-  const uint64_t k = keys[i];
   uint64_t kp = 0;
-  if (!is_reserved(k)) {
-    const KeyPos q = key_pos(t, k);
-    const int p = probe_find(t, q.b, q.start, q.d, k, false);
-    if (p >= 0) {
-      const uint64_t g = q.b * t.B + (uint32_t)p;
-      unsigned long long* ka = reinterpret_cast<unsigned long long*>(t.slots + 2 * g);
-      if (atomicCAS(ka, (unsigned long long)k, (unsigned long long)kLockedKey) ==
-          (unsigned long long)k) {
-        const bool has_in = scores != nullptr;
-        const uint64_t in = has_in ? scores[i] : 0;
-        bool w;
-        const uint64_t ns =
-            score_hit(sc, has_in, in, score_desired(sc, has_in, in), slot_score(t, g), &w);
-        if (w) slot_score(t, g) = ns;
-        kp = (uint64_t)(uintptr_t)ka;
-      }
+  if (p >= 0) {
+    const uint64_t g = b * t.B + (uint32_t)p;
+    unsigned long long* ka = reinterpret_cast<unsigned long long*>(t.slots + 2 * g);
+    if (atomicCAS(ka, (unsigned long long)k, (unsigned long long)kLockedKey) ==
+        (unsigned long long)k) {
+      const bool has_in = scores != nullptr;
+      const uint64_t in = has_in ? scores[i] : 0;
+      bool w;
+      const uint64_t ns =
+          score_hit(sc, has_in, in, score_desired(sc, has_in, in), slot_score(t, g), &w);
+      if (w) slot_score(t, g) = ns;
+      kp = (uint64_t)(uintptr_t)ka;
     }
   }
   kptrs[i] = kp;
@@ -3322,15 +3364,13 @@ __global__ __launch_bounds__(kBlock) void k_unlock_keys(TableView t, uint64_t n,
 // contains (contains_kernel.h:31-69): founds only.
 __global__ __launch_bounds__(kBlock) void k_contains(TableView t, const uint64_t* __restrict__ keys,
                                                      uint64_t n, uint8_t* __restrict__ founds) {
+  __shared__ ProbeLds s_probe[kBlock / 64];
   const uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
-  if (i >= n) return;
-  const uint64_t k = keys[i];
-  bool found = false;
-  if (!is_reserved(k)) {
-    const KeyPos q = key_pos(t, k);
-    found = probe_find(t, q.b, q.start, q.d, k, false) >= 0;
-  }
-  founds[i] = found ? 1 : 0;
+  const uint64_t k = i < n ? keys[i] : 0;
+  uint64_t b = 0;
+  const int p = wave_probe(t, k, i < n && !is_reserved(k), use_key_first(t),
+                           s_probe[threadIdx.x >> 6], &b);
+  if (i < n) founds[i] = p >= 0 ? 1 : 0;
 }
 
 // assign (assign_kernel.h:31-243) and assign_values
@@ -3343,28 +3383,25 @@ __global__ __launch_bounds__(kBlock) void k_assign(TableView t, const uint64_t* 
                                                    const uint64_t* __restrict__ scores,
                                                    ScoreCtx sc) {
   __shared__ uint32_t s_rows[kBlock / 64][64];
+  __shared__ ProbeLds s_probe[kBlock / 64];
   const uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
   const uint32_t wv = threadIdx.x >> 6;
+  const uint64_t k = i < n ? keys[i] : 0;
+  uint64_t b = 0;
+  const int p = wave_probe(t, k, i < n && !is_reserved(k), use_key_first(t), s_probe[wv], &b);
   uint64_t src = 0, dst = 0;
-  if (i < n) {
-    const uint64_t k = keys[i];
-    if (!is_reserved(k)) {
-      const KeyPos q = key_pos(t, k);
-      const int p = probe_find(t, q.b, q.start, q.d, k, false);
-      if (p >= 0) {
-        if (SCORES) {
-          const uint64_t g = q.b * t.B + (uint32_t)p;
-          const bool has_in = scores != nullptr;
-          bool w;
-          const uint64_t ns =
-              score_wo_missed(sc, has_in, has_in ? scores[i] : 0, slot_score(t, g), &w);
-          if (w) slot_score(t, g) = ns;
-        }
-        if (in_values) {
-          src = (uint64_t)(uintptr_t)(in_values + i * (uint64_t)t.row_bytes);
-          dst = (uint64_t)(uintptr_t)row_ptr(t, q.b, (uint32_t)p);
-        }
-      }
+  if (p >= 0) {
+    if (SCORES) {
+      const uint64_t g = b * t.B + (uint32_t)p;
+      const bool has_in = scores != nullptr;
+      bool w;
+      const uint64_t ns =
+          score_wo_missed(sc, has_in, has_in ? scores[i] : 0, slot_score(t, g), &w);
+      if (w) slot_score(t, g) = ns;
+    }
+    if (in_values) {
+      src = (uint64_t)(uintptr_t)(in_values + i * (uint64_t)t.row_bytes);
+      dst = (uint64_t)(uintptr_t)row_ptr(t, b, (uint32_t)p);
     }
   }
   wave_copy_pairs<U>(src, dst, t.row_bytes, s_rows[wv]);  // every lane of the wave

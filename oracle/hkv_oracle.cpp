@@ -850,24 +850,36 @@ int hkvo_assign_scores(hkvo_table* t, uint64_t n, const uint64_t* keys,
 int hkvo_find(hkvo_table* t, uint64_t n, const uint64_t* keys, void* values,
               uint8_t* founds, uint64_t* scores) {
   // include/kernels/find_kernel/find_with_digest_kernel.h:30-108; missed rows
-  // are left untouched.
-  for (uint64_t i = 0; i < n; i++) {
-    const uint64_t k = keys[i];
-    bool found = false;
-    if (!is_reserved(k)) {
-      uint64_t b;
-      uint32_t s;
-      uint8_t d;
-      t->locate_key(k, &b, &s, &d);
-      const int64_t p = t->find_slot(b, s, d, k);
-      if (p >= 0) {
-        found = true;
-        if (scores) scores[i] = t->scores[b * t->B + p];
-        std::memcpy((uint8_t*)values + i * t->row, t->rowp(b, (uint32_t)p), t->row);
+  // are left untouched.  Read-only, so in threaded mode each thread takes a
+  // contiguous range of the batch.
+  auto range = [&](uint64_t i0, uint64_t i1) {
+    for (uint64_t i = i0; i < i1; i++) {
+      const uint64_t k = keys[i];
+      bool found = false;
+      if (!is_reserved(k)) {
+        uint64_t b;
+        uint32_t s;
+        uint8_t d;
+        t->locate_key(k, &b, &s, &d);
+        const int64_t p = t->find_slot(b, s, d, k);
+        if (p >= 0) {
+          found = true;
+          if (scores) scores[i] = t->scores[b * t->B + p];
+          std::memcpy((uint8_t*)values + i * t->row, t->rowp(b, (uint32_t)p), t->row);
+        }
       }
+      if (founds) founds[i] = found ? 1 : 0;
     }
-    if (founds) founds[i] = found ? 1 : 0;
+  };
+  const uint64_t T = (uint64_t)std::max(1, t->threads);
+  if (T == 1 || n < 4096) {
+    range(0, n);
+    return HKVO_OK;
   }
+  std::vector<std::thread> th;
+  for (uint64_t j = 0; j < T; j++)
+    th.emplace_back(range, n * j / T, n * (j + 1) / T);
+  for (auto& x : th) x.join();
   return HKVO_OK;
 }
 

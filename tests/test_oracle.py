@@ -414,6 +414,10 @@ def test_threaded_mode_matches_single_thread():
     for a, b in zip(r0, r1):
         np.testing.assert_array_equal(a, b)
     _check_invariants(ts[0])
+    q = np.concatenate([prev, uniform_keys(rng, 7000)])
+    f0, f1 = (t.find(q, np.full((q.size, 4), 9, np.float32), with_scores=True) for t in ts)
+    for a, b in zip(f0, f1):
+        np.testing.assert_array_equal(a, b)
 
 
 def test_digest_and_tile_paths_place_identically_without_eviction():
