@@ -296,12 +296,14 @@ def bench_c5(torch, hkv_amd, stream, gen):
     return res
 
 
-def run_configs(torch, hkv_amd, stream, gen):
+def run_configs(torch, hkv_amd, stream, gen, only=None):
     import gc
     out = {}
-    for name, fn in (("zipf_epoch_lfu_cap2^27_dim32", bench_c3),
-                     ("lfu_full_table_cap2^26_dim128", bench_c4),
-                     ("hybrid_customized_cap2^27to2^28_dim64", bench_c5)):
+    for tag, name, fn in (("zipf", "zipf_epoch_lfu_cap2^27_dim32", bench_c3),
+                          ("lfu", "lfu_full_table_cap2^26_dim128", bench_c4),
+                          ("hybrid", "hybrid_customized_cap2^27to2^28_dim64", bench_c5)):
+        if only and tag != only:
+            continue
         try:
             out[name] = fn(torch, hkv_amd, stream, gen)
         except Exception as exc:  # reported, never fatal for the main line
@@ -406,6 +408,8 @@ def main():
     ap.add_argument("--configs-only", action="store_true",
                     help="run only the other benchmark configurations and print "
                          "their figures as one JSON object")
+    ap.add_argument("--only", choices=("zipf", "lfu", "hybrid"),
+                    help="with --configs-only: run just this configuration")
     ap.add_argument("--calibrate", action="store_true",
                     help="first run a plain 1 GiB device-to-device copy (the "
                          "reference kernel for scaling HBM byte counters)")
@@ -432,7 +436,7 @@ def main():
     gen = torch.Generator(device="cuda")
     gen.manual_seed(1234)
     if args.configs_only:
-        print(json.dumps(run_configs(torch, hkv_amd, stream, gen)), flush=True)
+        print(json.dumps(run_configs(torch, hkv_amd, stream, gen, args.only)), flush=True)
         return
     table = hkv_amd.HashTable("u64", "f32", hkv_amd.EvictStrategy.kLru)
     table.init(hkv_amd.HashTableOptions(

@@ -119,8 +119,21 @@ void launch_export(const TableView& t, uint64_t offset, uint64_t n,
                    hipStream_t s);
 void launch_size(const TableView& t, uint64_t nbuckets, uint64_t* out,
                  hipStream_t s);
-void launch_rehash(const TableView& t, uint64_t old_buckets, int unit,
-                   hipStream_t s);
+// Growth: the plan kernel rebuilds the old buckets' metadata and the new
+// buckets' (include/kernels/rehash_kernel/rehash_kernel.h:29-207) and
+// records the row moves; phase 0 of the row kernel moves rows to new buckets
+// and stages the ones that stay in their bucket, phase 1 writes the staged
+// rows back.
+struct RehashScratch {
+  uint16_t* rec;     // [old buckets * 128] row-move records
+  uint16_t* cnt;     // [old buckets] moves to the new bucket | moves within << 8
+  uint32_t* tbase;   // [old buckets] first staging row of the bucket
+  uint32_t* tcount;  // staging rows in all (zero before the plan kernel)
+};
+void launch_rehash_plan(const TableView& t, uint64_t old_buckets, const RehashScratch& rs,
+                        hipStream_t s);
+void launch_rehash_rows(const TableView& t, uint64_t old_buckets, const RehashScratch& rs,
+                        uint8_t* stage, int phase, int unit, hipStream_t s);
 void launch_fill_u64(uint64_t* p, uint64_t v, uint64_t n, hipStream_t s);
 void launch_fill_u32(uint32_t* p, uint32_t v, uint64_t n, hipStream_t s);
 

@@ -3543,81 +3543,236 @@ __global__ void k_fill_u32(uint32_t* p, uint32_t v, uint64_t n) {
     p[q] = v;
 }
 
-__device__ __forceinline__ void thread_copy(gptr<uint8_t> dst, gptr<const uint8_t> src,
-                                            uint32_t bytes, int unit) {
-  copy_row(dst, src, bytes, unit, 0, 1);
+/* ------------------------------------------------------------------------ */
+/* rehash (include/kernels/rehash_kernel/rehash_kernel.h:29-207)             */
+/* ------------------------------------------------------------------------ */
+//
+// k_rehash_plan: one 16-lane group per old bucket b replays the reference's
+// one-thread-per-bucket algorithm on the bucket held in registers (lane l
+// owns slots l + 16 j): scan from slot 0 for the first key whose bucket
+// under the doubled capacity is b + old_buckets, place it at the first
+// EMPTY slot of that bucket from its start, backward-shift defragment b
+// from the hole, and scan again from slot 0.  Each step is a few ballots
+// over per-slot flags instead of a chain of global loads.  Rows do not move
+// here: every slot tracks the slot its row started in, and the bucket's row
+// moves are recorded, as (first slot, destination) pairs, for
+// k_rehash_rows.
+//
+// Record of a row move: origin slot << 8 | (destination in b + old_buckets)
+// << 7 | destination slot, at rec[b * 128 + j]; cnt[b] = moves to the new
+// bucket | moves within b << 8 (new-bucket moves first).
+
+// Facts of the key a slot holds, moved with the key: start slot under the
+// old capacity (bits 0-6), start slot under the doubled capacity (8-14),
+// digest (16-23), whether it moves to the new bucket (24), whether the slot
+// holds a key (25).
+constexpr uint32_t kRhMove = 1u << 24, kRhLive = 1u << 25;
+
+__device__ __forceinline__ uint32_t rh_info(uint64_t k, uint64_t b, uint64_t old_cap,
+                                            uint64_t new_cap, uint32_t B) {
+  if (k == kEmptyKey) return 0;
+  const uint64_t h = murmur3(k);
+  const uint64_t ngi = h % new_cap;
+  const bool mv = k != kReclaimKey && ngi / B != b;  // RECLAIM slots are skipped by the scan
+  return (uint32_t)((h % old_cap) % B) | ((uint32_t)(ngi % B) << 8) | (key_digest(h) << 16) |
+         (mv ? kRhMove : 0u) | kRhLive;
 }
 
-// include/kernels/rehash_kernel/rehash_kernel.h:69-135 (backward-shift
-// defragmentation after a key leaves bucket b).
-__device__ void rehash_defrag(const TableView& t, uint64_t b, uint32_t remove_pos,
-                              uint64_t old_cap, int unit) {
-  const uint32_t B = t.B;
-  const uint64_t base = b * B;
-  uint32_t offset = 1;
-  while (offset < B) {
-    const uint32_t cur = (remove_pos + offset) % B;
-    const uint64_t ck = slot_key(t, base + cur);
-    if (ck == kEmptyKey) break;
-    const uint64_t h = murmur3(ck);
-    const uint64_t sp = (h % old_cap) % B;
-    if ((sp <= remove_pos && remove_pos < cur) || (cur < sp && sp <= remove_pos) ||
-        (remove_pos < cur && cur < sp)) {
-      slot_store(t, base + remove_pos, ck, slot_score(t, base + cur));
-      G(t.digests)[base + remove_pos] = (uint8_t)key_digest(h);
-      thread_copy(row_ptr(t, b, remove_pos), row_ptr(t, b, cur), t.row_bytes, unit);
-      slot_key(t, base + cur) = kEmptyKey;
-      G(t.digests)[base + cur] = kEmptyDigest;
-      remove_pos = cur;
-      offset = 1;
-    } else {
-      offset++;
-    }
+__device__ __forceinline__ uint32_t sel8(const uint32_t (&v)[8], uint32_t j) {
+  uint32_t r = 0;
+#pragma unroll
+  for (uint32_t q = 0; q < 8; q++) r |= v[q] & (0u - (uint32_t)(j == q));
+  return r;
+}
+
+__device__ __forceinline__ void set8(uint32_t (&v)[8], uint32_t j, uint32_t x) {
+#pragma unroll
+  for (uint32_t q = 0; q < 8; q++) v[q] = j == q ? x : v[q];
+}
+
+// 128-bit mask (lo, hi) of a 16-lane group's slots from per-lane flags
+// (bit j of f: slot l + 16 j).  Lanes of other groups that are not active
+// contribute nothing to this group's bits.
+__device__ __forceinline__ void group_mask128(uint32_t f, uint32_t gs, uint64_t& lo,
+                                              uint64_t& hi) {
+  lo = hi = 0;
+#pragma unroll
+  for (uint32_t j = 0; j < 8; j++) {
+    const uint64_t m = (__ballot((f >> j) & 1u) >> (16 * gs)) & 0xFFFFull;
+    if (j < 4) lo |= m << (16 * j);
+    else hi |= m << (16 * (j - 4));
   }
 }
 
-// include/kernels/rehash_kernel/rehash_kernel.h:137-207: one thread per old
-// bucket; keys whose bucket under the doubled capacity differs move to the
-// first EMPTY slot (circular from their start) of bucket b + old_buckets.
-__global__ __launch_bounds__(kBlock) void k_rehash(TableView t, uint64_t old_nb, int unit) {
-  const uint64_t b = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
-  if (b >= old_nb) return;
+__device__ __forceinline__ uint32_t ctz128(uint64_t lo, uint64_t hi) {
+  return lo ? (uint32_t)__builtin_ctzll(lo) : 64u + (uint32_t)__builtin_ctzll(hi);
+}
+
+__global__ __launch_bounds__(kBlock) void k_rehash_plan(TableView t, uint64_t old_nb,
+                                                        uint16_t* __restrict__ rec,
+                                                        uint16_t* __restrict__ cnt,
+                                                        uint32_t* __restrict__ tbase,
+                                                        uint32_t* __restrict__ tcount) {
+  const uint32_t lane = threadIdx.x & 63, l = lane & 15, gs = lane >> 4;
+  const uint64_t b = ((uint64_t)blockIdx.x * kBlock + threadIdx.x) >> 4;
+  if (b >= old_nb) return;  // group-uniform
   const uint32_t B = t.B;
-  const uint64_t base = b * B;
-  const uint64_t new_cap = t.capacity;
-  uint32_t kp = 0;
-  while (kp < B) {
-    const uint64_t ck = slot_key(t, base + kp);
-    if (ck == kEmptyKey || ck == kReclaimKey) {
-      kp++;
-      continue;
+  const uint64_t base = b * B, nbase = (b + old_nb) * B;
+  const uint64_t old_cap = old_nb * B, new_cap = t.capacity;
+  uint64_t key[8], score[8];
+  uint32_t info[8], org[8];
+#pragma unroll
+  for (uint32_t j = 0; j < 8; j++) {
+    const u64x2 r = slot_load(t, base + l + 16 * j);
+    key[j] = r.x;
+    score[j] = r.y;
+  }
+#pragma unroll
+  for (uint32_t j = 0; j < 8; j++) {
+    info[j] = rh_info(key[j], b, old_cap, new_cap, B);
+    org[j] = l + 16 * j;
+  }
+  uint64_t occ_lo = 0, occ_hi = 0;  // slots of the new bucket taken so far
+  uint32_t n_new = 0;
+  for (;;) {
+    uint32_t f = 0;
+#pragma unroll
+    for (uint32_t j = 0; j < 8; j++) f |= ((info[j] & kRhMove) ? 1u : 0u) << j;
+    uint64_t mlo, mhi;
+    group_mask128(f, gs, mlo, mhi);
+    if (!(mlo | mhi)) break;
+    // The first key to move, placed at the first free slot of the new
+    // bucket from its start there.
+    const uint32_t kp = ctz128(mlo, mhi);
+    const uint32_t ko = kp & 15, kj = kp >> 4;
+    const uint64_t mk = shfl_u64(rec_get(key, kj), (int)ko, 16);
+    const uint64_t ms = shfl_u64(rec_get(score, kj), (int)ko, 16);
+    const uint32_t mi = __shfl(sel8(info, kj), (int)ko, 16);
+    const uint32_t mo = __shfl(sel8(org, kj), (int)ko, 16);
+    const uint32_t nkp = (mi >> 8) & 127u;
+    uint64_t flo = ~occ_lo, fhi = ~occ_hi;
+    rot128(flo, fhi, nkp);
+    const uint32_t cp = (nkp + ctz128(flo, fhi)) & 127u;
+    if (cp < 64) occ_lo |= 1ull << cp;
+    else occ_hi |= 1ull << (cp - 64);
+    if (l == (cp & 15)) {
+      slot_store(t, nbase + cp, mk, ms);
+      G(t.digests)[nbase + cp] = (uint8_t)(mi >> 16);
     }
-    const uint64_t cs = slot_score(t, base + kp);
-    const uint64_t h = murmur3(ck);
-    const uint64_t ngi = h % new_cap;
-    const uint64_t nbk = ngi / B;
-    if (nbk == b) {
-      kp++;
-      continue;
+    if (l == 0) rec[b * B + n_new] = (uint16_t)((mo << 8) | 0x80u | cp);
+    n_new++;
+    if (l == ko) {
+      rec_set(key, kj, kEmptyKey);
+      set8(info, kj, 0u);
     }
-    const uint32_t nkp = (uint32_t)(ngi % B);
-    const uint64_t nbase = nbk * B;
-    for (uint32_t o = 0; o < B; o++) {
-      const uint32_t cp = (nkp + o) % B;
-      if (slot_key(t, nbase + cp) == kEmptyKey) {
-        slot_store(t, nbase + cp, ck, cs);
-        G(t.digests)[nbase + cp] = (uint8_t)key_digest(h);
-        G(t.bsize)[nbk]++;
-        thread_copy(row_ptr(t, nbk, cp), row_ptr(t, b, kp), t.row_bytes, unit);
-        break;
+    // Backward-shift defragmentation from the hole at rp: the first slot
+    // after rp (circularly) that is EMPTY ends it; the first key before that
+    // whose old start slot lies cyclically outside (rp, cur] fills the hole.
+    uint32_t rp = kp;
+    for (;;) {
+      uint32_t fe = 0, fc = 0;
+#pragma unroll
+      for (uint32_t j = 0; j < 8; j++) {
+        const uint32_t cur = l + 16 * j;
+        const bool live = (info[j] & kRhLive) != 0;
+        const uint32_t sp = info[j] & 127u;
+        const bool c = (sp <= rp && rp < cur) || (cur < sp && sp <= rp) || (rp < cur && cur < sp);
+        fe |= (live ? 0u : 1u) << j;
+        fc |= (live && c ? 1u : 0u) << j;
+      }
+      uint64_t elo, ehi, clo, chi;
+      group_mask128(fe, gs, elo, ehi);
+      group_mask128(fc, gs, clo, chi);
+      uint64_t xlo = elo | clo, xhi = ehi | chi;
+      const uint32_t sh = (rp + 1) & 127u;
+      rot128(xlo, xhi, sh);
+      xhi &= ~(1ull << 63);  // rp itself
+      if (!(xlo | xhi)) break;
+      const uint32_t q = (sh + ctz128(xlo, xhi)) & 127u;
+      const bool q_empty = q < 64 ? ((elo >> q) & 1) : ((ehi >> (q - 64)) & 1);
+      if (q_empty) break;
+      const uint32_t qo = q & 15, qj = q >> 4, ro = rp & 15, rj = rp >> 4;
+      const uint64_t vk = shfl_u64(rec_get(key, qj), (int)qo, 16);
+      const uint64_t vs = shfl_u64(rec_get(score, qj), (int)qo, 16);
+      const uint32_t vi = __shfl(sel8(info, qj), (int)qo, 16);
+      const uint32_t vo = __shfl(sel8(org, qj), (int)qo, 16);
+      if (l == ro) {
+        rec_set(key, rj, vk);
+        rec_set(score, rj, vs);
+        set8(info, rj, vi);
+        set8(org, rj, vo);
+      }
+      if (l == qo) {
+        rec_set(key, qj, kEmptyKey);
+        set8(info, qj, 0u);
+      }
+      rp = q;
+    }
+  }
+  // Write the bucket back; record the rows that end in another slot of b.
+  uint32_t fm = 0;
+#pragma unroll
+  for (uint32_t j = 0; j < 8; j++) {
+    const uint32_t s = l + 16 * j;
+    slot_store(t, base + s, key[j], score[j]);
+    G(t.digests)[base + s] = (info[j] & kRhLive) ? (uint8_t)(info[j] >> 16) : kEmptyDigest;
+    fm |= ((info[j] & kRhLive) && org[j] != s ? 1u : 0u) << j;
+  }
+  uint64_t ilo, ihi;
+  group_mask128(fm, gs, ilo, ihi);
+  const uint32_t n_int = __popcll(ilo) + __popcll(ihi);
+#pragma unroll
+  for (uint32_t j = 0; j < 8; j++) {
+    if ((fm >> j) & 1u) {
+      const uint32_t s = l + 16 * j;
+      const uint32_t below = s < 64 ? __popcll(ilo & ((1ull << s) - 1))
+                                    : __popcll(ilo) + __popcll(ihi & ((1ull << (s - 64)) - 1));
+      rec[b * B + n_new + below] = (uint16_t)((org[j] << 8) | s);
+    }
+  }
+  if (l == 0) {
+    cnt[b] = (uint16_t)(n_new | (n_int << 8));
+    if (n_new) {
+      G(t.bsize)[b] -= (int32_t)n_new;
+      G(t.bsize)[b + old_nb] = (int32_t)n_new;
+    }
+    tbase[b] = n_int ? atomicAdd(tcount, n_int) : 0u;
+  }
+}
+
+// Executes the recorded row moves, one lane per record, rows copied by the
+// wave together.  Phase 0 reads only rows in their first slots: it writes
+// the rows that go to new buckets and stages the rows that stay in their
+// bucket in `stage`; phase 1 writes the staged rows to their slots.
+template <int U>
+__global__ __launch_bounds__(kBlock) void k_rehash_rows(TableView t, uint64_t old_nb,
+                                                        const uint16_t* __restrict__ rec,
+                                                        const uint16_t* __restrict__ cnt,
+                                                        const uint32_t* __restrict__ tbase,
+                                                        uint8_t* __restrict__ stage, int phase) {
+  __shared__ uint32_t s_rows[kBlock / 64][64];
+  const uint32_t B = t.B, R = t.row_bytes;
+  const uint64_t x = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
+  uint64_t src = 0, dst = 0;
+  if (x < old_nb * B) {
+    const uint64_t b = x / B;
+    const uint32_t j = (uint32_t)(x % B);
+    const uint32_t c = cnt[b], nn = c & 0xFFu, ni = c >> 8;
+    if (j < nn + ni) {
+      const uint32_t r = rec[x], o = r >> 8, d = r & 127u;
+      const bool to_new = (r & 0x80u) != 0;
+      const uint64_t st = (uint64_t)(tbase[b] + (j - nn)) * R;
+      if (phase == 0) {
+        src = (uint64_t)(uintptr_t)row_ptr(t, b, o);
+        dst = to_new ? (uint64_t)(uintptr_t)row_ptr(t, b + old_nb, d)
+                     : (uint64_t)(uintptr_t)(stage + st);
+      } else if (!to_new) {
+        src = (uint64_t)(uintptr_t)(stage + st);
+        dst = (uint64_t)(uintptr_t)row_ptr(t, b, d);
       }
     }
-    slot_key(t, base + kp) = kEmptyKey;
-    G(t.digests)[base + kp] = kEmptyDigest;
-    G(t.bsize)[b]--;
-    rehash_defrag(t, b, kp, old_nb * B, unit);
-    kp = 0;
   }
+  wave_copy_pairs<U>(src, dst, R, s_rows[threadIdx.x >> 6]);
 }
 
 }  // namespace
@@ -3824,9 +3979,26 @@ void launch_size(const TableView& t, uint64_t nb, uint64_t* out, hipStream_t s) 
                      t.bsize, nb, reinterpret_cast<unsigned long long*>(out));
 }
 
-void launch_rehash(const TableView& t, uint64_t old_nb, int unit, hipStream_t s) {
-  hipLaunchKernelGGL(k_rehash, dim3(grid_for(old_nb, kBlock, 1ull << 31)), dim3(kBlock), 0, s, t,
-                     old_nb, unit);
+void launch_rehash_plan(const TableView& t, uint64_t old_nb, const RehashScratch& rs,
+                        hipStream_t s) {
+  hipLaunchKernelGGL(k_rehash_plan, dim3(grid_for(old_nb * 16, kBlock, 1ull << 31)),
+                     dim3(kBlock), 0, s, t, old_nb, rs.rec, rs.cnt, rs.tbase, rs.tcount);
+}
+
+void launch_rehash_rows(const TableView& t, uint64_t old_nb, const RehashScratch& rs,
+                        uint8_t* stage, int phase, int unit, hipStream_t s) {
+  const dim3 g(grid_for(old_nb * t.B, kBlock, 1ull << 31)), b(kBlock);
+#define HKV_RH_U(UU)                                                                        \
+  hipLaunchKernelGGL((k_rehash_rows<UU>), g, b, 0, s, t, old_nb, rs.rec, rs.cnt, rs.tbase, \
+                     stage, phase)
+  switch (unit) {
+    case 16: HKV_RH_U(16); break;
+    case 8: HKV_RH_U(8); break;
+    case 4: HKV_RH_U(4); break;
+    case 2: HKV_RH_U(2); break;
+    default: HKV_RH_U(1); break;
+  }
+#undef HKV_RH_U
 }
 
 }  // namespace hkv

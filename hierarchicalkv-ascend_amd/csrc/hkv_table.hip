@@ -461,9 +461,50 @@ struct hkv_table {
     set_capacity(2 * old_C);
     add_slices(old_nb, nb, s);
     launch_init_slots(view(), old_nb, nb, s);
-    launch_rehash(view(), old_nb, value_unit(nullptr), s);
-    hip_check(hipGetLastError(), "rehash launch");
-    hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
+    // Metadata first, with the row moves recorded; then the rows.
+    RehashScratch rs{};
+    uint8_t* stage = nullptr;
+    bool stage_host = false;
+    try {
+      hip_check(hipMalloc(&rs.rec, old_C * sizeof(uint16_t)), "hipMalloc(rehash records)");
+      hip_check(hipMalloc(&rs.cnt, old_nb * sizeof(uint16_t)), "hipMalloc(rehash counts)");
+      hip_check(hipMalloc(&rs.tbase, old_nb * sizeof(uint32_t)), "hipMalloc(rehash bases)");
+      hip_check(hipMalloc(&rs.tcount, sizeof(uint32_t)), "hipMalloc(rehash counter)");
+      launch_fill_u32(rs.tcount, 0, 1, s);
+      launch_rehash_plan(view(), old_nb, rs, s);
+      hip_check(hipGetLastError(), "rehash launch");
+      uint32_t staged = 0;
+      hip_check(hipMemcpyAsync(&staged, rs.tcount, sizeof(staged), hipMemcpyDeviceToHost, s),
+                "hipMemcpyAsync");
+      hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
+      if (staged) {
+        // Rows that stay in their bucket pass through a staging buffer: HBM
+        // when it can be had, else pinned host memory.
+        if (hipMalloc(&stage, (uint64_t)staged * row) != hipSuccess) {
+          (void)hipGetLastError();
+          hip_check(hipHostMalloc(&stage, (uint64_t)staged * row, hipHostMallocDefault),
+                    "hipHostMalloc(rehash staging)");
+          stage_host = true;
+        }
+      }
+      const int unit = value_unit(nullptr);
+      launch_rehash_rows(view(), old_nb, rs, stage, 0, unit, s);
+      if (staged) launch_rehash_rows(view(), old_nb, rs, stage, 1, unit, s);
+      hip_check(hipGetLastError(), "rehash launch");
+      hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
+    } catch (...) {
+      (void)hipFree(rs.rec);
+      (void)hipFree(rs.cnt);
+      (void)hipFree(rs.tbase);
+      (void)hipFree(rs.tcount);
+      if (stage) (void)(stage_host ? hipHostFree(stage) : hipFree(stage));
+      throw;
+    }
+    (void)hipFree(rs.rec);
+    (void)hipFree(rs.cnt);
+    (void)hipFree(rs.tbase);
+    (void)hipFree(rs.tcount);
+    if (stage) (void)(stage_host ? hipHostFree(stage) : hipFree(stage));
   }
 
   // include/hkv_hashtable.h:2873-2935
