@@ -47,6 +47,28 @@ struct ApplyArgs {
   int value_type;  // for accumulation
 };
 
+// Listed partitions with more than kBigPart entries of a batch with repeated
+// keys (Zipf traffic) are counted, folded and tasked over the whole GPU; one
+// slot of per-partition state each, at most kBigMax per call (others take
+// the in-block path).
+constexpr uint32_t kBigPart = 4096;
+constexpr uint32_t kBigMax = 256;
+constexpr uint32_t kBigMapCap = 1024;  // distinct keys of a partition's heavy buckets
+constexpr uint32_t kBigLight = 1024;   // other entries, run by one LDS run
+struct BigSlot {
+  uint32_t tot[256];                // entries per bucket of the partition
+  uint64_t mkey[kBigMapCap];        // key map: key (EMPTY: free),
+  uint64_t msum[kBigMapCap];        // fold of the input scores,
+  uint32_t mfirst[kBigMapCap];      // first and last batch index,
+  uint32_t mlast[kBigMapCap];
+  uint32_t mres[kBigMapCap];        // placement (slot | new / placed flags)
+  uint32_t mfull;                   // a key did not fit the map
+  uint32_t nlight;                  // entries of the other buckets
+  uint32_t fast;                    // k_apply_part left the row tasks to k_big_tasks
+  uint32_t pad;
+  uint64_t light[2 * kBigLight];    // those entries, {key, batch index}
+};
+
 // Per-call scratch of the partitioned apply pipeline (owned by the table).
 // A partition is a run of 256 consecutive buckets; the batch is cut into
 // chunks of 1024 keys.  Segment (g, p) = the keys of chunk g that fall in
@@ -60,11 +82,13 @@ struct PartScratch {
   uint32_t* plist;      // [partitions] partitions the single-run kernel left
   uint32_t* drec;       // [n][4] buckets handed to the 16-lane kernel
   uint64_t* dpool;      // [n][2] their keys, {key, batch index}
-  uint32_t* dctr;       // [4] records, pool entries, listed partitions, partitions taken
-                        // (zeroed by the count kernel)
+  uint32_t* dctr;       // [8] records, pool entries, listed partitions, partitions taken,
+                        // big partitions listed (zeroed by the count kernel)
   uint32_t* ev_bits;    // [n / 32 + 1] insert_and_evict record flags, zero between calls
   uint32_t* ev_wpre;    // [n / 32 + 1] set bits before each word, within its block of 256 words
   uint32_t* ev_blk;     // [n / 8192 + 3] block offsets, then the record count and records below it
+  BigSlot* big;         // [kBigMax] big-partition state (null: that path is off)
+  uint32_t* big_part;   // [kBigMax] partition of each big slot
   uint32_t np;          // partitions
   uint32_t prange;      // partitions per counting pass (LDS histogram size)
   uint32_t chunks;      // batch chunks

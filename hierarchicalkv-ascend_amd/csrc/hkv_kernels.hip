@@ -1029,6 +1029,7 @@ __global__ __launch_bounds__(kBlock) void k_pcount(TableView t, const uint64_t* 
     ps.dctr[1] = 0;
     ps.dctr[2] = 0;
     ps.dctr[3] = 0;
+    ps.dctr[4] = 0;
   }
   uint32_t* H = ps.hist + (uint64_t)blockIdx.x * NP;
   for (uint32_t p0 = 0; p0 < NP; p0 += ps.prange) {
@@ -1428,6 +1429,8 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
   __shared__ uint32_t s_head[kPartBuckets];  // first key map entry of each heavy bucket
   __shared__ uint64_t s_rbase[kPartBuckets];  // row 0 of each bucket (heavy-bucket copies)
   __shared__ uint32_t s_hw[kHvPer][kBlock / 64];  // kept entries per sub-tile and wave
+  __shared__ int32_t s_bslot;     // big slot of the partition (-1: none)
+  __shared__ uint32_t s_anyser;   // a heavy bucket was left to the serial walk
   // Key map {key, fold sum, first / last batch index, result, bucket}.
   uint64_t* const mkey = reinterpret_cast<uint64_t*>(s_dg);
   uint64_t* const msum = mkey + kMapCap;
@@ -1461,10 +1464,27 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
     const uint32_t base_e = ps.pinfo[2 * p], m = ps.pinfo[2 * p + 1];
     const uint64_t part_b0 = (uint64_t)p * kPartBuckets;
     uint32_t m_run = m;  // entries left to the run loop
+    gptr<const u64x2> rent = ent;  // entries of the run loop
+    uint32_t run_base = base_e;
     if constexpr (kDeferRows) {
+      // A big partition's counts and key map were built grid-wide.
+      if (tid == 0) {
+        s_bslot = -1;
+        s_anyser = 0;
+      }
+      __syncthreads();
+      if (ps.big) {
+        uint32_t nbb = *(volatile uint32_t*)&ps.dctr[4];
+        nbb = nbb < kBigMax ? nbb : kBigMax;
+        for (uint32_t q = tid; q < nbb; q += kBlock)
+          if (ps.big_part[q] == p) s_bslot = (int32_t)q;
+      }
+      __syncthreads();
+      const int32_t bslot = s_bslot;
+      BigSlot* const bs = bslot >= 0 ? ps.big + bslot : nullptr;
       /* H0. Entries per bucket over the whole partition (a wave adds the
          count of its leading lane's bucket with one atomic). */
-      s_tot[tid] = 0;
+      s_tot[tid] = bs ? bs->tot[tid] : 0u;
       s_hst[tid] = kHvNone;
       s_rbase[tid] = part_b0 + tid < t.buckets
                          ? (uint64_t)(uintptr_t)row_ptr(t, part_b0 + tid, 0) : 0;
@@ -1474,7 +1494,7 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
         s_kept = 0;
       }
       __syncthreads();
-      for (uint32_t e0 = 0; e0 < m; e0 += kBlock * kHvPer) {
+      for (uint32_t e0 = 0; !bs && e0 < m; e0 += kBlock * kHvPer) {
         uint64_t kq[kHvPer];
 #pragma unroll
         for (uint32_t r = 0; r < kHvPer; r++) {
@@ -1504,14 +1524,28 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
         const bool sum_in = a.sc.strategy == kLfu || a.sc.strategy == kEpochLfu;
         const bool fold_ok =
             has_in || !(sum_in || a.sc.strategy == kCustomized);
-        /* H1. Fold the heavy buckets' entries into the key map. */
+        /* H1. Fold the heavy buckets' entries into the key map (for a big
+           partition: load the map folded grid-wide and link its keys into
+           their buckets' lists). */
         for (uint32_t q = tid; q < kMapCap; q += kBlock) {
-          mkey[q] = kEmptyKey;
-          msum[q] = 0;
-          mfirst[q] = kNone;
-          mlast[q] = 0;
+          mkey[q] = bs ? bs->mkey[q] : kEmptyKey;
+          msum[q] = bs ? bs->msum[q] : 0;
+          mfirst[q] = bs ? bs->mfirst[q] : kNone;
+          mlast[q] = bs ? bs->mlast[q] : 0;
         }
+        if (bs && tid == 0) s_mfull = bs->mfull;
         __syncthreads();
+        if (bs) {
+          for (uint32_t q = tid; q < kMapCap; q += kBlock) {
+            const uint64_t k = mkey[q];
+            if (k != kEmptyKey) {
+              const uint32_t bk = (uint32_t)(bucket_of(t, k) % kPartBuckets);
+              mnext[q] = (uint16_t)atomicExch(&s_head[bk], q);
+              mbk[q] = (uint8_t)bk;
+            }
+          }
+          __syncthreads();
+        }
         // The next tile's entries load while this tile's input scores are
         // gathered (their addresses depend on the entries).
         u64x2 nq[kHvPer];
@@ -1520,9 +1554,9 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
           const uint32_t e = tid + r * kBlock;
           nq[r].x = kEmptyKey;
           nq[r].y = 0;
-          if (e < m) nq[r] = ent[base_e + e];
+          if (!bs && e < m) nq[r] = ent[base_e + e];
         }
-        for (uint32_t e0 = 0; e0 < m; e0 += kBlock * kHvPer) {
+        for (uint32_t e0 = 0; !bs && e0 < m; e0 += kBlock * kHvPer) {
           if (*(volatile uint32_t*)&s_mfull) break;  // block-uniform: set before a barrier
           u64x2 eq[kHvPer];
           uint64_t hq_[kHvPer], cq[kHvPer];
@@ -1769,10 +1803,24 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
           }
         }
         __syncthreads();
+        if (s_hst[tid] == kHvSerial) s_anyser = 1;
+        __syncthreads();
+        // A big partition whose heavy buckets were all folded and whose other
+        // entries fit one run leaves the row work to k_big_tasks and runs the
+        // entries k_big_fold listed.
+        const bool big_fast = bs && !s_mfull && !s_anyser && bs->nlight <= kBigLight;
+        if (big_fast) {
+          for (uint32_t q = tid; q < kMapCap; q += kBlock)
+            if (mkey[q] != kEmptyKey) bs->mres[q] = mres[q];
+          if (tid == 0) bs->fast = 1;
+          rent = G(reinterpret_cast<const u64x2*>(bs->light));
+          run_base = 0;
+          m_run = bs->nlight;
+        }
         /* H3. Row copies of the folded buckets' occurrences (find_or_insert:
            row tasks), and the other entries compacted in place (order kept)
            for the run loop. */
-        for (uint32_t e0 = 0; e0 < m; e0 += kBlock * kHvPer) {
+        for (uint32_t e0 = 0; !big_fast && e0 < m; e0 += kBlock * kHvPer) {
           u64x2 eq[kHvPer];
           uint64_t srcq[kHvPer], dstq[kHvPer];
           bool keepq[kHvPer];
@@ -1838,12 +1886,12 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
           if (tid == 0) s_kept = run;
         }
         __syncthreads();
-        m_run = s_kept;
+        if (!big_fast) m_run = s_kept;
         __syncthreads();
       }
     }
-    uint32_t c0 = base_e;
-    const uint32_t end_e = base_e + m_run;
+    uint32_t c0 = run_base;
+    const uint32_t end_e = run_base + m_run;
     while (c0 < end_e) {
       // This run of entries: the whole list when it fits, else whole
       // segments in chunk order.  A segment holds at most kPartChunk =
@@ -1853,7 +1901,7 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
         if (tid == 0) s_c1 = c0;
         __syncthreads();
         for (uint32_t x = c0 + 1 + tid; x <= c0 + kPartLds; x += kBlock)
-          if (ent[x].y / kPartChunk != ent[x - 1].y / kPartChunk) atomicMax(&s_c1, x);
+          if (rent[x].y / kPartChunk != rent[x - 1].y / kPartChunk) atomicMax(&s_c1, x);
         __syncthreads();
       }
       if (tid == 0) {
@@ -1867,7 +1915,7 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
       const uint32_t mc = c1 - c0;
       // Group the run's entries by bucket.
       for (uint32_t e = tid; e < mc; e += kBlock)
-        atomicAdd(&s_cnt[bucket_of(t, ent[c0 + e].x) % kPartBuckets], 1u);
+        atomicAdd(&s_cnt[bucket_of(t, rent[c0 + e].x) % kPartBuckets], 1u);
       __syncthreads();
       {
         const uint32_t v = s_cnt[tid];
@@ -1886,7 +1934,7 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
       }
       __syncthreads();
       for (uint32_t e = tid; e < mc; e += kBlock) {
-        const u64x2 v = ent[c0 + e];
+        const u64x2 v = rent[c0 + e];
         const uint32_t pos = atomicAdd(&s_fill[bucket_of(t, v.x) % kPartBuckets], 1u);
         s_key[pos] = v.x;
         s_idx[pos] = (uint32_t)v.y;
@@ -2149,6 +2197,318 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
 // in all, the k-th record at a position >= c moves into the k-th hole below
 // c (sources and destinations are disjoint, so every move runs in
 // parallel), the counter gets c, and the flags are cleared.
+/* ------------------------------------------------------------------------ */
+/* big partitions of batches with repeated keys                              */
+/* ------------------------------------------------------------------------ */
+//
+// A partition that receives more than kBigPart entries of a batch with
+// repeated keys (Zipf traffic, where one key can occur tens of thousands of
+// times) would leave one block of k_apply_part streaming all of its entries
+// three times: entries per bucket (H0), the heavy-bucket fold (H1) and the
+// per-occurrence row work (H3).  k_apply_fast lists such partitions in
+// big slots, and these passes run over the whole GPU instead, with each
+// partition's counts and key map in its slot in global memory:
+//   k_big_clear  resets the listed slots;
+//   k_big_count  adds up entries per bucket;
+//   k_big_fold   folds the heavy buckets' entries into the key map (first
+//                and last batch index and score sum per key: associative,
+//                so the order in which blocks fold does not matter) and
+//                lists the other entries;
+//   k_apply_part loads the counts and the map, places the heavy buckets'
+//                keys (H2) and applies the listed entries in its run loop;
+//   k_big_tasks  does H3's work: per-occurrence row tasks (find_or_insert)
+//                or the last occurrence's row copy.
+// If the map overflows, a heavy bucket cannot be folded (H2 leaves it to the
+// serial walk) or the other entries exceed one LDS run, k_apply_part
+// finishes the partition with its own H3 and run loop, and k_big_tasks
+// skips it.
+
+constexpr uint32_t kBigTile = kBlock * kHvPer;  // entries per tile of the grid-wide passes
+static_assert(kBigMapCap == kMapCap && kBigLight == kPartLds && kBigMax == kBlock,
+              "big-partition slot layout");
+
+// Tiles of the listed big partitions: s_pre[s] = tiles of slots before s
+// (s_pre[nb] = all of them).  Every thread of the block calls this.
+__device__ __forceinline__ uint32_t big_tiles(const PartScratch& ps, uint32_t* s_pre,
+                                              uint32_t* s_wsum, uint32_t* nb_out) {
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  uint32_t nb = *(volatile uint32_t*)&ps.dctr[4];
+  nb = nb < kBigMax ? nb : kBigMax;
+  uint32_t c = 0;
+  if (tid < nb) c = (ps.pinfo[2 * ps.big_part[tid] + 1] + kBigTile - 1) / kBigTile;
+  uint32_t x = c;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t y = __shfl_up(x, d, 64);
+    if (lane >= (uint32_t)d) x += y;
+  }
+  if (lane == 63) s_wsum[wv] = x;
+  __syncthreads();
+  uint32_t pre = 0;
+  for (uint32_t q = 0; q < wv; q++) pre += s_wsum[q];
+  s_pre[tid + 1] = pre + x;
+  if (tid == 0) s_pre[0] = 0;
+  __syncthreads();
+  *nb_out = nb;
+  return s_pre[nb];
+}
+
+// Slot of tile v: the last s with s_pre[s] <= v.
+__device__ __forceinline__ uint32_t big_slot_of(const uint32_t* s_pre, uint32_t nb, uint32_t v) {
+  uint32_t lo = 0, hi = nb;  // s_pre[lo] <= v < s_pre[hi]
+  while (hi - lo > 1) {
+    const uint32_t mid = (lo + hi) >> 1;
+    if (s_pre[mid] <= v) lo = mid;
+    else hi = mid;
+  }
+  return lo;
+}
+
+__global__ __launch_bounds__(kBlock) void k_big_clear(PartScratch ps) {
+  const uint32_t s = blockIdx.x, tid = threadIdx.x;
+  const uint32_t nb = *(volatile uint32_t*)&ps.dctr[4];
+  if (s >= nb || s >= kBigMax) return;
+  BigSlot& S = ps.big[s];
+  S.tot[tid] = 0;
+  for (uint32_t q = tid; q < kBigMapCap; q += kBlock) {
+    S.mkey[q] = kEmptyKey;
+    S.msum[q] = 0;
+    S.mfirst[q] = kNone;
+    S.mlast[q] = 0;
+  }
+  if (tid == 0) {
+    S.mfull = 0;
+    S.nlight = 0;
+    S.fast = 0;
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void k_big_count(TableView t, PartScratch ps) {
+  __shared__ uint32_t s_pre[kBigMax + 1], s_wsum[kBlock / 64], s_cnt[kPartBuckets];
+  const uint32_t tid = threadIdx.x;
+  uint32_t nb;
+  const uint32_t total = big_tiles(ps, s_pre, s_wsum, &nb);
+  gptr<const u64x2> ent = G(reinterpret_cast<const u64x2*>(ps.ent));
+  for (uint32_t v = blockIdx.x; v < total; v += gridDim.x) {
+    const uint32_t sl = big_slot_of(s_pre, nb, v);
+    const uint32_t p = ps.big_part[sl];
+    const uint32_t base_e = ps.pinfo[2 * p], m = ps.pinfo[2 * p + 1];
+    const uint32_t e0 = (v - s_pre[sl]) * kBigTile;
+    uint64_t kq[kHvPer];
+#pragma unroll
+    for (uint32_t r = 0; r < kHvPer; r++) {
+      const uint32_t e = e0 + tid + r * kBlock;
+      kq[r] = e < m ? ent[base_e + e].x : kEmptyKey;
+    }
+    s_cnt[tid] = 0;
+    __syncthreads();
+#pragma unroll
+    for (uint32_t r = 0; r < kHvPer; r++)
+      if (e0 + tid + r * kBlock < m) atomicAdd(&s_cnt[bucket_of(t, kq[r]) % kPartBuckets], 1u);
+    __syncthreads();
+    if (s_cnt[tid]) atomicAdd(&ps.big[sl].tot[tid], s_cnt[tid]);
+    __syncthreads();
+  }
+}
+
+template <int OP>
+__global__ __launch_bounds__(kBlock) void k_big_fold(TableView t, ApplyArgs a, PartScratch ps) {
+  __shared__ uint32_t s_pre[kBigMax + 1], s_wsum[kBlock / 64], s_tot[kPartBuckets];
+  const uint32_t tid = threadIdx.x, lane = tid & 63;
+  uint32_t nb;
+  const uint32_t total = big_tiles(ps, s_pre, s_wsum, &nb);
+  gptr<const u64x2> ent = G(reinterpret_cast<const u64x2*>(ps.ent));
+  const bool has_in = a.in_scores != nullptr;
+  const bool sum_in = a.sc.strategy == kLfu || a.sc.strategy == kEpochLfu;
+  for (uint32_t v = blockIdx.x; v < total; v += gridDim.x) {
+    const uint32_t sl = big_slot_of(s_pre, nb, v);
+    BigSlot& S = ps.big[sl];
+    const uint32_t p = ps.big_part[sl];
+    const uint32_t base_e = ps.pinfo[2 * p], m = ps.pinfo[2 * p + 1];
+    const uint32_t e0 = (v - s_pre[sl]) * kBigTile;
+    u64x2 eq[kHvPer];
+    uint64_t hq_[kHvPer], cq[kHvPer];
+    bool hvq[kHvPer], ltq[kHvPer];
+#pragma unroll
+    for (uint32_t r = 0; r < kHvPer; r++) {
+      const uint32_t e = e0 + tid + r * kBlock;
+      eq[r].x = kEmptyKey;
+      eq[r].y = 0;
+      if (e < m) eq[r] = ent[base_e + e];
+    }
+#pragma unroll
+    for (uint32_t r = 0; r < kHvPer; r++) {
+      cq[r] = 0;
+      if (sum_in && has_in && e0 + tid + r * kBlock < m) cq[r] = G(a.in_scores)[eq[r].y];
+    }
+    s_tot[tid] = S.tot[tid];
+    __syncthreads();
+#pragma unroll
+    for (uint32_t r = 0; r < kHvPer; r++) {
+      const bool valid = e0 + tid + r * kBlock < m;
+      hq_[r] = murmur3(eq[r].x);
+      const uint32_t bk = (uint32_t)((global_idx(t, hq_[r]) >> t.bshift) % kPartBuckets);
+      hvq[r] = valid && s_tot[bk] > kHeavyMin;
+      ltq[r] = valid && !hvq[r];
+      const uint64_t in = cq[r];
+      cq[r] = !hvq[r] ? 0 : a.sc.strategy == kLfu ? in : (in & kScoreMask);
+    }
+    // Other buckets' entries: listed, one atomic per wave and sub-tile.
+#pragma unroll
+    for (uint32_t r = 0; r < kHvPer; r++) {
+      const uint64_t lm = __ballot(ltq[r]);
+      if (lm) {
+        uint32_t base = 0;
+        if (lane == 0) base = atomicAdd(&S.nlight, (uint32_t)__popcll(lm));
+        base = __shfl(base, 0, 64);
+        const uint32_t pos = base + (uint32_t)__popcll(lm & ((1ull << lane) - 1));
+        if (ltq[r] && pos < kBigLight) {
+          S.light[2 * pos] = eq[r].x;
+          S.light[2 * pos + 1] = eq[r].y;
+        }
+      }
+    }
+    // Heavy entries: the wave's leading key folded over the tile with one
+    // reduction, then the map updated once for it and once per other entry.
+    uint64_t lk = 0;
+    bool have_lead = false;
+#pragma unroll
+    for (uint32_t r = 0; r < kHvPer; r++) {
+      const uint64_t act = __ballot(hvq[r]);
+      if (act && !have_lead) {
+        lk = shfl_u64(eq[r].x, __ffsll((unsigned long long)act) - 1, 64);
+        have_lead = true;
+      }
+    }
+    uint32_t l1 = kNone, l2 = 0;
+    uint64_t l3 = 0;
+    if (have_lead) {
+#pragma unroll
+      for (uint32_t r = 0; r < kHvPer; r++) {
+        if (hvq[r] && eq[r].x == lk) {
+          const uint32_t i = (uint32_t)eq[r].y;
+          l1 = i < l1 ? i : l1;
+          l2 = i > l2 ? i : l2;
+          l3 += cq[r];
+          hvq[r] = false;
+        }
+      }
+#pragma unroll
+      for (int d = 32; d > 0; d >>= 1) {
+        const uint32_t o1 = __shfl_xor(l1, d, 64), o2 = __shfl_xor(l2, d, 64);
+        l1 = o1 < l1 ? o1 : l1;
+        l2 = o2 > l2 ? o2 : l2;
+        l3 += shfl_xor_u64(l3, d, 64);
+      }
+    }
+#pragma unroll
+    for (uint32_t r = 0; r <= kHvPer; r++) {
+      bool mine;
+      uint64_t k, h, csum;
+      uint32_t fmin, fmax;
+      if (r == kHvPer) {
+        mine = have_lead && lane == 0;
+        k = lk;
+        h = murmur3(lk);
+        fmin = l1;
+        fmax = l2;
+        csum = l3;
+      } else {
+        mine = hvq[r];
+        k = eq[r].x;
+        h = hq_[r];
+        fmin = fmax = (uint32_t)eq[r].y;
+        csum = cq[r];
+      }
+      if (mine) {
+        uint32_t q = map_home(h);
+        bool ok = false;
+        for (uint32_t pr = 0; pr < kMapProbe; pr++) {
+          const uint64_t cur = atomicCAS(reinterpret_cast<unsigned long long*>(&S.mkey[q]),
+                                         (unsigned long long)kEmptyKey, (unsigned long long)k);
+          if (cur == kEmptyKey || cur == k) {
+            ok = true;
+            break;
+          }
+          q = (q + 1) & (kBigMapCap - 1);
+        }
+        if (!ok) {
+          atomicOr(&S.mfull, 1u);
+        } else {
+          atomicMin(&S.mfirst[q], fmin);
+          atomicMax(&S.mlast[q], fmax);
+          if (csum) atomicAdd(reinterpret_cast<unsigned long long*>(&S.msum[q]),
+                              (unsigned long long)csum);
+        }
+      }
+    }
+    __syncthreads();  // s_tot of the next tile
+  }
+}
+
+template <int OP, int U>
+__global__ __launch_bounds__(kBlock) void k_big_tasks(TableView t, ApplyArgs a, PartScratch ps) {
+  __shared__ uint32_t s_pre[kBigMax + 1], s_wsum[kBlock / 64], s_tot[kPartBuckets];
+  __shared__ uint32_t s_rows[kBlock / 64][64];
+  const uint32_t tid = threadIdx.x, wv = tid >> 6;
+  uint32_t nb;
+  const uint32_t total = big_tiles(ps, s_pre, s_wsum, &nb);
+  gptr<const u64x2> ent = G(reinterpret_cast<const u64x2*>(ps.ent));
+  gptr<uint64_t> trow = G(ps.trow);
+  const uint32_t R = t.row_bytes;
+  for (uint32_t v = blockIdx.x; v < total; v += gridDim.x) {
+    const uint32_t sl = big_slot_of(s_pre, nb, v);
+    const BigSlot& S = ps.big[sl];
+    if (!*(volatile const uint32_t*)&S.fast) continue;  // block-uniform
+    const uint32_t p = ps.big_part[sl];
+    const uint32_t base_e = ps.pinfo[2 * p], m = ps.pinfo[2 * p + 1];
+    const uint64_t part_b0 = (uint64_t)p * kPartBuckets;
+    const uint32_t e0 = (v - s_pre[sl]) * kBigTile;
+    u64x2 eq[kHvPer];
+    uint64_t srcq[kHvPer], dstq[kHvPer];
+#pragma unroll
+    for (uint32_t r = 0; r < kHvPer; r++) {
+      const uint32_t e = e0 + tid + r * kBlock;
+      eq[r].x = kEmptyKey;
+      eq[r].y = 0;
+      if (e < m) eq[r] = ent[base_e + e];
+    }
+    s_tot[tid] = S.tot[tid];
+    __syncthreads();
+#pragma unroll
+    for (uint32_t r = 0; r < kHvPer; r++) {
+      const uint64_t k = eq[r].x, i = eq[r].y;
+      const uint64_t h = murmur3(k);
+      const uint64_t gb = global_idx(t, h) >> t.bshift;
+      const uint32_t bk = (uint32_t)(gb % kPartBuckets);
+      srcq[r] = dstq[r] = 0;
+      // In a slot left to this kernel every heavy bucket was folded.
+      if (e0 + tid + r * kBlock < m && s_tot[bk] > kHeavyMin) {
+        uint32_t q = map_home(h);
+        uint32_t pr = 0;
+        while (S.mkey[q] != k && pr < kBigMapCap) {  // present: folded
+          q = (q + 1) & (kBigMapCap - 1);
+          pr++;
+        }
+        if (S.mkey[q] != k) continue;
+        const uint32_t rs = S.mres[q];
+        const uint64_t trow_a = (uint64_t)(uintptr_t)row_ptr(t, part_b0 + bk, rs & (t.B - 1));
+        if (OP == OP_FIND_OR_INSERT) {
+          const uint32_t first = S.mfirst[q];
+          trow[i] = !(rs & kMapNew) ? (kTaskOut | trow_a)
+                    : i == first ? (kTaskIn | trow_a)
+                                 : (kTaskFwd | (uint64_t)first);
+        } else if (i == S.mlast[q]) {
+          srcq[r] = (uint64_t)(uintptr_t)(a.in_values + i * R);
+          dstq[r] = trow_a;
+        }
+      }
+    }
+    wave_copy_tasks<U, kHvPer>(srcq, dstq, R, s_rows[wv]);
+    __syncthreads();  // s_tot of the next tile
+  }
+}
+
 constexpr uint32_t kEvBlkWords = 256;  // bitmap words per block of the count kernel
 
 __device__ __forceinline__ uint32_t block_excl_scan256(uint32_t v, uint32_t* s_w,
@@ -2622,7 +2982,13 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
   const uint32_t p = blockIdx.x;
   const uint32_t base_e = ps.pinfo[2 * p], m = ps.pinfo[2 * p + 1];
   if (m > kFastLds) {
-    if (tid == 0) ps.plist[atomicAdd(&ps.dctr[2], 1u)] = p;  // k_apply_part takes it
+    if (tid == 0) {
+      ps.plist[atomicAdd(&ps.dctr[2], 1u)] = p;  // k_apply_part takes it
+      if (ps.big && m > kBigPart) {
+        const uint32_t sl = atomicAdd(&ps.dctr[4], 1u);
+        if (sl < kBigMax) ps.big_part[sl] = p;
+      }
+    }
     return;
   }
   if (m == 0) return;
@@ -3853,15 +4219,26 @@ static void apply_part_op(const TableView& t, const ApplyArgs& a, const PartScra
   hipLaunchKernelGGL(k_pscatter, dim3(ps.chunks), dim3(kBlock), lds, s, t, a.keys, a.n, ps);
   const dim3 g(ps.np), b(kBlock);
   // After the single-run kernel, the eviction path and the multi-run kernel
-  // walk device-side lists that are usually empty: small grids.
+  // walk device-side lists that are usually empty: small grids.  Two blocks
+  // of the multi-run kernel fit a CU (LDS and registers), so 512 of them
+  // take its listed partitions two per CU at a time.
   const dim3 gd(grid_for(a.n * 16, kBlock, 2048));
-  const dim3 gp(ps.np < 256 ? ps.np : 256);
+  const dim3 gp(ps.np < 512 ? ps.np : 512);
   const uint32_t nw = (uint32_t)((a.n + 31) / 32);
   const uint32_t nbw = (nw + kEvBlkWords - 1) / kEvBlkWords;
+  // Big partitions: at most n / kBigPart of them, kBigTile entries per tile.
+  const dim3 gb(grid_for(a.n / kBigTile + kBigMax, 1, 1024));
 #define HKV_PART_U(UU)                                                                       \
   hipLaunchKernelGGL((k_apply_fast<OP, UU>), g, b, 0, s, t, a, ps);                          \
   hipLaunchKernelGGL((k_apply_deferred<OP, UU>), gd, b, 0, s, t, a, ps);                     \
+  if (ps.big) {                                                                              \
+    hipLaunchKernelGGL(k_big_clear, dim3(kBigMax), b, 0, s, ps);                              \
+    hipLaunchKernelGGL(k_big_count, gb, b, 0, s, t, ps);                                     \
+    hipLaunchKernelGGL((k_big_fold<OP>), gb, b, 0, s, t, a, ps);                             \
+  }                                                                                          \
   hipLaunchKernelGGL((k_apply_part<OP, UU>), gp, b, 0, s, t, a, ps);                         \
+  if (ps.big && OP != OP_ASSIGN_SCORES)                                                      \
+    hipLaunchKernelGGL((k_big_tasks<OP, UU>), gb, b, 0, s, t, a, ps);                        \
   if (OP == OP_FIND_OR_INSERT)                                                               \
     hipLaunchKernelGGL((k_rowtasks<UU>), dim3(grid_for(a.n, kBlock, 2048)), b, 0, s, t, a, ps); \
   if (OP == OP_INSERT_AND_EVICT && a.ev_bits) {                                              \

@@ -170,6 +170,8 @@ struct hkv_table {
   uint32_t* p_evwpre = nullptr;
   uint32_t* p_evblk = nullptr;
   uint64_t p_evw_cap = 0;
+  BigSlot* p_big = nullptr;
+  uint32_t* p_bigpart = nullptr;
   // export scratch
   uint32_t* blk = nullptr;
   uint64_t blk_cap = 0;
@@ -289,6 +291,8 @@ struct hkv_table {
     (void)hipFree(p_evbits);
     (void)hipFree(p_evwpre);
     (void)hipFree(p_evblk);
+    (void)hipFree(p_big);
+    (void)hipFree(p_bigpart);
     (void)hipFree(blk);
     (void)hipFree(d_sum);
     if (h_sum) (void)hipHostFree(h_sum);
@@ -321,7 +325,7 @@ struct hkv_table {
     auto* list = reinterpret_cast<uint32_t*>(take(L.np * 4));
     auto* drec = reinterpret_cast<uint32_t*>(take(n * 16));
     auto* dpool = reinterpret_cast<uint64_t*>(take(n * 16));
-    auto* dctr = reinterpret_cast<uint32_t*>(take(16));
+    auto* dctr = reinterpret_cast<uint32_t*>(take(32));
     auto* spill = reinterpret_cast<uint32_t*>(take(4));
     if (off > kNoAllocScratchBytes)
       fail(HKV_ERR_INVALID,
@@ -329,10 +333,20 @@ struct hkv_table {
                " MiB of scratch on this table; the static scratch array holds " +
                std::to_string(kNoAllocScratchBytes >> 20) + " MiB");
     launch_fill_u64(trow, 0, n, s);
-    *ps = PartScratch{hist,    ent,     info,         spill,      trow,
-                      list,    drec,    dpool,        dctr,       nullptr,
-                      nullptr, nullptr, (uint32_t)L.np, part_range, (uint32_t)L.ng,
-                      (uint32_t)L.cap};
+    *ps = PartScratch{};
+    ps->hist = hist;
+    ps->ent = ent;
+    ps->pinfo = info;
+    ps->spill_top = spill;
+    ps->trow = trow;
+    ps->plist = list;
+    ps->drec = drec;
+    ps->dpool = dpool;
+    ps->dctr = dctr;
+    ps->np = (uint32_t)L.np;
+    ps->prange = part_range;
+    ps->chunks = (uint32_t)L.ng;
+    ps->cap = (uint32_t)L.cap;
   }
 
   // Sizes of the partitioned apply path's scratch for a batch of n keys.
@@ -403,7 +417,7 @@ struct hkv_table {
       hip_check(hipMalloc(&p_dpool, n * 16), "hipMalloc(defer pool)");
       p_defer_cap = n;
     }
-    if (!p_dctr) hip_check(hipMalloc(&p_dctr, 4 * sizeof(uint32_t)), "hipMalloc(part counters)");
+    if (!p_dctr) hip_check(hipMalloc(&p_dctr, 8 * sizeof(uint32_t)), "hipMalloc(part counters)");
     const uint64_t nw = n / 32 + 1;
     if (nw > p_evw_cap) {
       if (p_evbits) hip_check(hipFree(p_evbits), "hipFree");
@@ -415,10 +429,33 @@ struct hkv_table {
       launch_fill_u32(p_evbits, 0, nw, s);
       p_evw_cap = nw;
     }
-    *ps = PartScratch{p_hist,   p_ent,   p_info,       p_spill,    p_trow,
-                      p_list,   p_drec,  p_dpool,      p_dctr,     p_evbits,
-                      p_evwpre, p_evblk, (uint32_t)np, part_range, (uint32_t)ng,
-                      (uint32_t)cap};
+    *ps = PartScratch{};
+    ps->hist = p_hist;
+    ps->ent = p_ent;
+    ps->pinfo = p_info;
+    ps->spill_top = p_spill;
+    ps->trow = p_trow;
+    ps->plist = p_list;
+    ps->drec = p_drec;
+    ps->dpool = p_dpool;
+    ps->dctr = p_dctr;
+    ps->ev_bits = p_evbits;
+    ps->ev_wpre = p_evwpre;
+    ps->ev_blk = p_evblk;
+    ps->np = (uint32_t)np;
+    ps->prange = part_range;
+    ps->chunks = (uint32_t)ng;
+    ps->cap = (uint32_t)cap;
+  }
+
+  // State of the big-partition path (batches with repeated keys).
+  void big_scratch(PartScratch* ps) {
+    if (!p_big) {
+      hip_check(hipMalloc(&p_big, kBigMax * sizeof(BigSlot)), "hipMalloc(big partitions)");
+      hip_check(hipMalloc(&p_bigpart, kBigMax * sizeof(uint32_t)), "hipMalloc(big partitions)");
+    }
+    ps->big = p_big;
+    ps->big_part = p_bigpart;
   }
 
   uint64_t sampled_size(hipStream_t s) {
@@ -609,8 +646,15 @@ int insert_like(hkv_table* t, int op, uint64_t n, const void* keys, const void* 
   a.unit = min_unit(t, {in_values, io_values, ev_values});
   a.value_type = t->value_type;
   PartScratch ps{};
-  if (given) ps = *given;
-  else t->part_scratch(n, &ps, s);
+  if (given) {
+    ps = *given;
+  } else {
+    t->part_scratch(n, &ps, s);
+    // Batches with repeated keys may hold hot keys: their big partitions
+    // are counted and folded grid-wide (accum_or_assign accumulates in
+    // batch order inside one block instead).
+    if (rule == RULE_TILE32 && op != OP_ACCUM_OR_ASSIGN) t->big_scratch(&ps);
+  }
   if (op == OP_INSERT_AND_EVICT) a.ev_bits = ps.ev_bits;
   launch_apply_part(t->view(), op, a, ps, s);
   hip_check(hipGetLastError(), "kernel launch");
