@@ -30,13 +30,19 @@ DIM = 64
 BATCH = 1 << 20
 
 
-# HBM bytes per key that each operation's kernels move at this workload, from
-# rocprofv3 FETCH_SIZE and WRITE_SIZE passes over
-# `bench.py --no-cpu-baseline --no-extra --no-configs --steps 4 --warmup 1 --calibrate`,
-# scaled by the factors a plain 1 GiB device copy gives in the same run
-# (fetch x2.0, write x1.0); the per-kernel figures are in
-# profiles/insert_or_assign_find_cap64M_dim64_hbm_bytes.md.
-MEASURED_BYTES_PER_KEY = {"insert_new": 735.7, "find_hit": 661.7}
+# HBM bytes per key that each operation's kernels move at this workload,
+# measured by rocprofv3 FETCH_SIZE and WRITE_SIZE passes (scaled by what the
+# same counters read for a plain 1 GiB device copy) and kept, with the
+# command that measured them, in profiles/hbm_traffic.json.
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+
+
+def measured_bytes_per_key(op):
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return json.load(f)["bytes_per_key"][op]
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def algo_bytes(op, dim=DIM):
@@ -296,6 +302,45 @@ def bench_c5(torch, hkv_amd, stream, gen):
     return res
 
 
+def bench_at_load_factor(torch, hkv_amd, stream, gen, target, calls=3):
+    """The headline table (kLru, 2^26 slots, dim 64) filled with batches of
+    2^20 new keys to the load factor `target`, then `calls` insert_or_assign
+    calls of new keys and `calls` find calls of keys just inserted, each
+    timed with events on the stream they run on.  Counter passes read the
+    last `calls` dispatches of each kernel."""
+    t = hkv_amd.HashTable("u64", "f32", hkv_amd.EvictStrategy.kLru)
+    t.init(hkv_amd.HashTableOptions(init_capacity=CAP, max_capacity=CAP,
+                                    max_hbm_for_vectors=CAP * DIM * 4, dim=DIM))
+    vals = torch.rand((BATCH, DIM), device="cuda", generator=gen) * 2 - 1
+    out = torch.empty((BATCH, DIM), dtype=torch.float32, device="cuda")
+    fnd = torch.empty(BATCH, dtype=torch.uint8, device="cuda")
+    with torch.cuda.stream(stream):
+        guard = 0
+        while t.load_factor(stream) < target - 1e-9 and guard < 200:
+            if target < 1.0 and t.load_factor(stream) + BATCH / CAP > target:
+                break
+            t.insert_or_assign(BATCH, rand_keys(torch, BATCH, gen), vals, None, stream)
+            guard += 1
+        lf0 = t.load_factor(stream)
+        ks = [rand_keys(torch, BATCH, gen) for _ in range(calls)]
+        e = _events(torch, 2 * calls + 1)
+        torch.cuda.synchronize()
+        for r in range(calls):
+            e[r].record(stream)
+            t.insert_or_assign(BATCH, ks[r], vals, None, stream)
+        e[calls].record(stream)
+        for r in range(calls):
+            t.find(BATCH, ks[r], out, fnd, None, stream)
+            e[calls + 1 + r].record(stream)
+        torch.cuda.synchronize()
+    ins = [e[r].elapsed_time(e[r + 1]) for r in range(calls)]
+    fi = [e[calls + r].elapsed_time(e[calls + 1 + r]) for r in range(calls)]
+    del t
+    return {"load_factor_at_start": round(lf0, 4),
+            "insert_or_assign_ms": [round(x, 4) for x in ins],
+            "find_hit_ms": [round(x, 4) for x in fi], "hits_last": int(fnd.sum().item())}
+
+
 def run_configs(torch, hkv_amd, stream, gen, only=None):
     import gc
     out = {}
@@ -410,6 +455,9 @@ def main():
                          "their figures as one JSON object")
     ap.add_argument("--only", choices=("zipf", "lfu", "hybrid"),
                     help="with --configs-only: run just this configuration")
+    ap.add_argument("--at-load-factor", type=float, default=None,
+                    help="only: fill the headline table to this load factor, then "
+                         "time 3 insert_or_assign and 3 find calls (counter passes)")
     ap.add_argument("--calibrate", action="store_true",
                     help="first run a plain 1 GiB device-to-device copy (the "
                          "reference kernel for scaling HBM byte counters)")
@@ -435,6 +483,10 @@ def main():
     stream = torch.cuda.Stream(device=dev)
     gen = torch.Generator(device="cuda")
     gen.manual_seed(1234)
+    if args.at_load_factor is not None:
+        print(json.dumps(bench_at_load_factor(torch, hkv_amd, stream, gen,
+                                              args.at_load_factor)), flush=True)
+        return
     if args.configs_only:
         print(json.dumps(run_configs(torch, hkv_amd, stream, gen, args.only)), flush=True)
         return
@@ -651,7 +703,8 @@ def main():
         roof = {"kernel": "find (k_find)", "achieved": round(find_gbs, 1),
                 "bytes_per_key": algo_bytes("find_hit"),
                 "ms_per_launch": round(find_ms, 4), "op": "find_hit"}
-    traffic = round(MEASURED_BYTES_PER_KEY[roof["op"]] * BATCH)
+    bpk = measured_bytes_per_key(roof["op"])
+    traffic = round(bpk * BATCH) if bpk is not None else None
     roofline = {"bound": "hbm", "achieved": roof["achieved"], "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(roof["achieved"] / HBM_PEAK_GBS, 4),
                 "traffic": traffic, "traffic_unit": "bytes per launch (rocprofv3 "

@@ -4219,11 +4219,13 @@ static void apply_part_op(const TableView& t, const ApplyArgs& a, const PartScra
   hipLaunchKernelGGL(k_pscatter, dim3(ps.chunks), dim3(kBlock), lds, s, t, a.keys, a.n, ps);
   const dim3 g(ps.np), b(kBlock);
   // After the single-run kernel, the eviction path and the multi-run kernel
-  // walk device-side lists that are usually empty: small grids.  Two blocks
-  // of the multi-run kernel fit a CU (LDS and registers), so 512 of them
-  // take its listed partitions two per CU at a time.
+  // walk device-side lists that are usually empty: small grids.  Batches
+  // with repeated keys list many partitions (every bucket with more than 32
+  // keys lists its partition); two blocks of the multi-run kernel fit a CU
+  // (LDS and registers), so for them 512 blocks take the list two per CU.
   const dim3 gd(grid_for(a.n * 16, kBlock, 2048));
-  const dim3 gp(ps.np < 512 ? ps.np : 512);
+  const uint32_t gpn = a.rule == RULE_TILE32 ? 512u : 256u;
+  const dim3 gp(ps.np < gpn ? ps.np : gpn);
   const uint32_t nw = (uint32_t)((a.n + 31) / 32);
   const uint32_t nbw = (nw + kEvBlkWords - 1) / kEvBlkWords;
   // Big partitions: at most n / kBigPart of them, kBigTile entries per tile.
