@@ -133,6 +133,20 @@ struct hkv_table {
   uint64_t B = 128, nb = 0, C = 0, row = 0;
   uint64_t qd_magic = 0, qd_shift = 0;
   bool reach_max = false;
+  // Upper bound on the occupancy sum that fast_load_factor reads (the first
+  // min(buckets, 1024) bucket sizes), kept on the host so that a call whose
+  // bound cannot exceed max_load_factor skips the stream synchronisation of
+  // the exact sum; the growth decision is the same either way, since the
+  // load factor rises with the sum.  The bound starts from an exact sum and
+  // grows by each insert-like call's batch size (a call raises the sum by at
+  // most that); erase only lowers the true sum; growth and clear drop it.
+  // It is used only while every insert-like call comes on one stream: work
+  // queued on another stream before an exact sum would escape the bound.
+  uint64_t samp_hi = 0;
+  bool samp_ok = false;
+  bool samp_off = false;
+  bool samp_has_stream = false;
+  hipStream_t samp_stream = nullptr;
   uint64_t epoch = kIgnoredEpoch;
   bool clock_override = false;
   uint64_t clock_value = 0;
@@ -468,11 +482,28 @@ struct hkv_table {
     return *h_sum;
   }
 
-  // fast_load_factor (include/hkv_hashtable.h:3229-3268).
-  float fast_load_factor(uint64_t delta, hipStream_t s) {
+  // fast_load_factor (include/hkv_hashtable.h:3229-3268) for a given sum of
+  // the first min(buckets, 1024) bucket sizes.
+  float fast_load_factor_of(uint64_t delta, uint64_t tot) const {
     const uint64_t N = std::min<uint64_t>(nb, 1024);
-    const uint64_t tot = sampled_size(s);
     return (float)((delta * 1.0) / (C * 1.0) + (tot * 1.0) / (B * N * 1.0));
+  }
+
+  // Every insert-like call passes its stream here; a second stream turns
+  // the host-side bound off for the table's lifetime.
+  void note_stream(hipStream_t s) {
+    if (!samp_has_stream) {
+      samp_has_stream = true;
+      samp_stream = s;
+    } else if (s != samp_stream) {
+      samp_off = true;
+    }
+  }
+
+  // After an insert-like call of n keys has been queued.
+  void note_insert(uint64_t n) {
+    const uint64_t most = B * std::min<uint64_t>(nb, 1024);
+    samp_hi = (n >= most - std::min(samp_hi, most)) ? most : samp_hi + n;
   }
 
   void double_capacity(hipStream_t s) {
@@ -495,6 +526,7 @@ struct hkv_table {
     slots = nsl;
     bsize = nbs;
     nb = 2 * old_nb;
+    samp_ok = false;
     set_capacity(2 * old_C);
     add_slices(old_nb, nb, s);
     launch_init_slots(view(), old_nb, nb, s);
@@ -556,8 +588,21 @@ struct hkv_table {
     reach_max = (C * 2 > opt.max_capacity);
   }
 
+  // The auto-grow loop of the insert-like calls (include/hkv_hashtable.h:
+  // 1103-1106, 1278-1281, 1456-1459, 1535-1538, 1669-1672), then the bound
+  // update.
   void maybe_grow(uint64_t n, hipStream_t s) {
-    while (!reach_max && fast_load_factor(n, s) > opt.max_load_factor) reserve(C * 2, s);
+    note_stream(s);
+    while (!reach_max) {
+      if (samp_ok && !samp_off && fast_load_factor_of(n, samp_hi) <= opt.max_load_factor)
+        break;
+      const uint64_t tot = sampled_size(s);
+      samp_hi = tot;
+      samp_ok = true;
+      if (fast_load_factor_of(n, tot) <= opt.max_load_factor) break;
+      reserve(C * 2, s);
+    }
+    note_insert(n);
   }
 
   // check_evict_strategy (include/hkv_hashtable.h:3270-3298), plus a check
@@ -819,6 +864,8 @@ int hkv_insert_or_assign_noalloc(hkv_table* t, uint64_t n, const void* keys,
            "insert_or_assign_noalloc needs a table at its maximum capacity "
            "(growing the table allocates)");
     t->check_scores(st, scores, ignore_evict_strategy != 0);
+    t->note_stream(S(stream));
+    t->note_insert(n);
     PartScratch ps{};
     t->noalloc_scratch(n, &ps, S(stream));
     insert_like(t, OP_INSERT_OR_ASSIGN, n, keys, values, nullptr, scores, nullptr, nullptr,
@@ -939,6 +986,7 @@ int hkv_erase(hkv_table* t, uint64_t n, const void* keys, hkv_stream stream) {
 int hkv_clear(hkv_table* t, hkv_stream stream) {
   return guarded([&] {
     need_table(t);
+    t->samp_ok = false;
     launch_clear(t->view(), S(stream));
     hip_check(hipGetLastError(), "clear launch");
   });

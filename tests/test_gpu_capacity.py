@@ -19,6 +19,7 @@ import numpy as np
 import pytest
 
 import oracle as O
+import gpu_pair
 from gpu_pair import Pair, records_equal
 from helpers import uniform_keys, zipf_keys
 
@@ -123,4 +124,47 @@ def test_multi_pass_partition_counting(monkeypatch, prange):
         ov, gv = p.find_or_insert(ks, rand_vals(rng, ks.size, 4),
                                   np.ones(ks.size, np.uint64), unique_key=False)
         np.testing.assert_array_equal(gv.view(np.uint32), ov.view(np.uint32))
+    p.assert_same_state()
+
+
+def test_auto_grow_decisions_small_batches():
+    """Auto-grow with batches of 1-300 keys (include/hkv_hashtable.h:
+    1103-1106).  The table keeps a host-side upper bound on the sampled
+    bucket sizes and synchronises for the exact sum only when the bound could
+    cross max_load_factor; the capacity after every call must still be the
+    oracle's.  Erases, a clear, a reserve and calls on a second stream (which
+    turn the bound off) are mixed in."""
+    rng = np.random.default_rng(91)
+    dim = 4
+    p = Pair(1024, max_capacity=1 << 16, dim=dim, strategy=O.LFU)
+    torch = p.torch
+    resident = np.empty(0, np.uint64)
+    side = torch.cuda.Stream()
+    for step in range(700):
+        n = int(rng.integers(1, 301))
+        ks = uniform_keys(rng, n)
+        v = rand_vals(rng, n, dim)
+        sc = rng.integers(1, 1 << 40, n, dtype=np.uint64)
+        if step < 600:
+            if step % 3 == 0:
+                p.find_or_insert(ks, v, sc)
+            else:
+                p.insert_or_assign(ks, v, sc)
+        else:
+            p.o.insert_or_assign(ks, v, sc, True, False, 12345)
+            with torch.cuda.stream(side):
+                kd, vd, sd = gpu_pair.to_dev(ks), gpu_pair.to_dev(v), gpu_pair.to_dev(sc)
+                p.g.insert_or_assign(n, kd, vd, sd, side.cuda_stream, True, False)
+            side.synchronize()
+        resident = np.concatenate([resident, ks])
+        if step % 50 == 49:
+            gone = rng.choice(resident, resident.size // 3, replace=False)
+            p.erase(gone)
+            resident = np.setdiff1d(resident, gone)
+        if step == 300:
+            p.clear()
+            resident = np.empty(0, np.uint64)
+        if step == 450:
+            p.reserve(p.g.capacity() * 2)
+        assert p.g.capacity() == p.o.capacity(), step
     p.assert_same_state()
