@@ -991,6 +991,9 @@ __device__ __forceinline__ bool lane_step(const TableView& t, const ApplyArgs& a
 constexpr uint32_t kPartLds = kPartChunk;  // entries one LDS load holds
 constexpr uint32_t kDgStride = 33;         // words per bucket digest row in LDS
 constexpr uint32_t kLaneMax = 32;          // keys per bucket the lane pass takes
+// Listed-partition flag: k_apply_fast applied every bucket of the partition
+// with at most kLaneMax keys, and k_apply_part takes only the others.
+constexpr uint32_t kPartLongOnly = 0x80000000u;
 constexpr uint32_t kPartTaskCap = 128;     // queued row tasks per wave
 
 __device__ __forceinline__ uint64_t bucket_of(const TableView& t, uint64_t k) {
@@ -1460,7 +1463,12 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
     __syncthreads();
     const uint32_t li = s_li;
     if (li >= nlist) break;  // block-uniform
-    const uint32_t p = ps.plist[li];
+    const uint32_t pl = ps.plist[li];
+    // kPartLongOnly: k_apply_fast applied the buckets with at most kLaneMax
+    // entries; only the longer ones are folded (or walked) here.
+    const bool long_only = (pl & kPartLongOnly) != 0;
+    const uint32_t p = pl & ~kPartLongOnly;
+    const uint32_t hmin = long_only ? kLaneMax : kHeavyMin;  // heavy: more entries than this
     const uint32_t base_e = ps.pinfo[2 * p], m = ps.pinfo[2 * p + 1];
     const uint64_t part_b0 = (uint64_t)p * kPartBuckets;
     uint32_t m_run = m;  // entries left to the run loop
@@ -1517,9 +1525,10 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
       }
       __syncthreads();
       s_head[tid] = kNone;
-      if (s_tot[tid] > kHeavyMin) s_hlist[atomicAdd(&s_nheavy, 1u)] = (uint8_t)tid;
+      if (s_tot[tid] > hmin) s_hlist[atomicAdd(&s_nheavy, 1u)] = (uint8_t)tid;
       __syncthreads();
       const uint32_t nheavy = s_nheavy;
+      if (long_only && !nheavy) m_run = 0;  // nothing left (not expected)
       if (nheavy) {
         const bool sum_in = a.sc.strategy == kLfu || a.sc.strategy == kEpochLfu;
         const bool fold_ok =
@@ -1580,7 +1589,7 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
           for (uint32_t r = 0; r < kHvPer; r++) {
             hq_[r] = murmur3(eq[r].x);
             const uint32_t bk = (uint32_t)((global_idx(t, hq_[r]) >> t.bshift) % kPartBuckets);
-            hvq[r] = e0 + tid + r * kBlock < m && s_tot[bk] > kHeavyMin;
+            hvq[r] = e0 + tid + r * kBlock < m && s_tot[bk] > hmin;
           }
 #pragma unroll
           for (uint32_t r = 0; r < kHvPer; r++) {
@@ -1858,7 +1867,7 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
             }
             srcq[r] = src;
             dstq[r] = dst;
-            keepq[r] = v && !done;
+            keepq[r] = v && !done && (!long_only || s_tot[bk] > kLaneMax);
           }
           uint64_t kmq[kHvPer];
 #pragma unroll
@@ -2954,6 +2963,7 @@ __device__ __forceinline__ void emit_fast(const TableView& t, const ApplyArgs& a
 template <int OP, int U>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_apply_fast(TableView t, ApplyArgs a, PartScratch ps) {
   constexpr uint32_t kPer = (kFastLds + kBlock - 1) / kBlock;  // entries per thread
+  constexpr bool kSplitLong = OP != OP_ACCUM_OR_ASSIGN;
   constexpr bool may_insert = OP != OP_ASSIGN_SCORES;
   constexpr bool moves_rows = OP != OP_ASSIGN_SCORES;
   constexpr bool reads_rows = OP == OP_FIND_OR_INSERT;
@@ -2973,6 +2983,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
   __shared__ uint32_t s_rows[kBlock / 64][64];
   __shared__ uint32_t s_wsum[kBlock / 64];
   __shared__ uint32_t s_big;
+  __shared__ uint8_t s_long[kPartBuckets];  // buckets left to k_apply_part (long buckets)
   __shared__ uint32_t s_nrec, s_npool;  // hand-over records and pool entries of the block
   __shared__ uint8_t s_serial[kPartBuckets];  // buckets left to the serial lanes
   __shared__ uint8_t s_isser[kPartBuckets];   // 1 for those buckets
@@ -2980,18 +2991,18 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
   __shared__ uint32_t s_rbase, s_pbase;
   const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const uint32_t p = blockIdx.x;
-  const uint32_t base_e = ps.pinfo[2 * p], m = ps.pinfo[2 * p + 1];
-  if (m > kFastLds) {
+  const uint32_t base_e = ps.pinfo[2 * p], m_all = ps.pinfo[2 * p + 1];
+  if (m_all > kFastLds) {
     if (tid == 0) {
       ps.plist[atomicAdd(&ps.dctr[2], 1u)] = p;  // k_apply_part takes it
-      if (ps.big && m > kBigPart) {
+      if (ps.big && m_all > kBigPart) {
         const uint32_t sl = atomicAdd(&ps.dctr[4], 1u);
         if (sl < kBigMax) ps.big_part[sl] = p;
       }
     }
     return;
   }
-  if (m == 0) return;
+  if (m_all == 0) return;
   const uint32_t B = t.B;
   const uint64_t part_b0 = (uint64_t)p * kPartBuckets;
   const bool has_in = a.in_scores != nullptr;
@@ -2999,7 +3010,13 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
   const bool old_for_new = a.sc.strategy == kLfu && !has_in;
 
   /* A. Entries grouped by bucket (every load issued before the first use;
-        indices past m read entry m - 1 and are ignored). */
+        indices past m_all read entry m_all - 1 and are ignored).  A bucket
+        with more than kLaneMax keys is left to k_apply_part, which folds
+        repeated keys: its entries are dropped here (buckets are independent,
+        so the rest of the partition is applied as usual), and the partition
+        is listed with kPartLongOnly.  accum_or_assign lists the whole
+        partition instead (k_apply_part applies its accumulations in batch
+        order without a fold). */
   {
     const uint64_t b = part_b0 + tid;
     const uint32_t bsz_own = b < t.buckets ? (uint32_t)G(t.bsize)[b] : 0u;
@@ -3010,7 +3027,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
 #pragma unroll
     for (uint32_t q = 0; q < kPer; q++) {
       const uint32_t e = tid + q * kBlock;
-      ev[q] = ent[e < m ? e : m - 1];
+      ev[q] = ent[e < m_all ? e : m_all - 1];
     }
 #pragma unroll
     for (uint32_t q = 0; q < kPer; q++) inq[q] = has_in ? G(a.in_scores)[ev[q].y] : 0;
@@ -3028,9 +3045,12 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
     lds_barrier();
 #pragma unroll
     for (uint32_t q = 0; q < kPer; q++)
-      if (tid + q * kBlock < m) atomicAdd(&s_cnt[lb[q]], 1u);
+      if (tid + q * kBlock < m_all) atomicAdd(&s_cnt[lb[q]], 1u);
     lds_barrier();
-    const uint32_t c = s_cnt[tid];
+    const bool lng = kSplitLong && s_cnt[tid] > kLaneMax;
+    const uint32_t c = lng ? 0u : s_cnt[tid];
+    s_long[tid] = lng ? 1 : 0;
+    if (lng) s_big = 2;
     uint32_t x = c;
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
@@ -3045,16 +3065,17 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
     const uint32_t o = pre + x - c;
     s_off[tid] = o;
     s_cnt[tid] = o;  // fill pointer (this thread read its count above)
-    if (tid == 0) s_off[kPartBuckets] = m;
+    if (tid == kBlock - 1) s_off[kPartBuckets] = o + c;
     lds_barrier();
-    if (s_big) {
-      // A long bucket: k_apply_part orders it.
+    if (s_big == 1) {
+      // A long bucket: k_apply_part orders the partition.
       if (tid == 0) ps.plist[atomicAdd(&ps.dctr[2], 1u)] = p;
       return;
     }
+    if (s_big == 2 && tid == 0) ps.plist[atomicAdd(&ps.dctr[2], 1u)] = p | kPartLongOnly;
 #pragma unroll
     for (uint32_t q = 0; q < kPer; q++) {
-      if (tid + q * kBlock < m) {
+      if (tid + q * kBlock < m_all && !s_long[lb[q]]) {
         s_idx[atomicAdd(&s_cnt[lb[q]], 1u)] = (uint32_t)ev[q].y;
       }
     }
@@ -3063,7 +3084,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
     // Batch order inside each bucket: every entry moves to lo + its rank.
 #pragma unroll
     for (uint32_t q = 0; q < kPer; q++) {
-      if (tid + q * kBlock < m) {
+      if (tid + q * kBlock < m_all && !s_long[lb[q]]) {
         const uint32_t lo = s_off[lb[q]], hi = s_off[lb[q] + 1];
         const uint32_t iv = (uint32_t)ev[q].y;
         uint32_t r = 0;
@@ -3074,7 +3095,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
     lds_barrier();
 #pragma unroll
     for (uint32_t q = 0; q < kPer; q++) {
-      if (tid + q * kBlock < m) {
+      if (tid + q * kBlock < m_all && !s_long[lb[q]]) {
         s_key[pos[q]] = ev[q].x;
         s_idx[pos[q]] = (uint32_t)ev[q].y;
         s_sc[pos[q]] = inq[q];
@@ -3082,6 +3103,9 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
     }
     lds_barrier();
   }
+  // Entries kept here (all of them unless long buckets were dropped).
+  const uint32_t m = s_off[kPartBuckets];
+  if (m == 0) return;  // block-uniform
 
   /* B. Outcome of every key on the table before the call, with the score,
         metadata record and row task it has if the parallel pass applies it. */

@@ -180,3 +180,73 @@ def test_single_key_repeated_many_times():
             q = np.concatenate([np.repeat(k, 50000), light])
             q = q[rng.permutation(q.size)]
             _run(p, "find_or_insert", rng, q, strategy, dim, clock=5 + r)
+
+
+def _long_bucket_batch(rng, p, cap, dim, strategy):
+    """Batches whose partitions (256 buckets) hold at most 704 entries but
+    some buckets more than 32: k_apply_fast applies the short buckets and
+    lists the partition for its long ones only.  Bucket kinds: a few hot keys
+    (present and new) repeated; 40 distinct new keys once each; a nearly full
+    bucket given 5 new hot keys (no fold: the batch-order walk, with
+    eviction); 140 distinct keys (more than a bucket holds)."""
+    nb = cap // 128
+    parts = rng.choice(nb // 256, 12, replace=False)
+    fill, batch = [], []
+    for j, part in enumerate(parts):
+        b = int(part) * 256 + int(rng.integers(0, 256))
+        kind = j % 4
+        if kind == 0:
+            ks = keys_in_bucket(rng, 4, cap, b, lo=1 << 40, hi=1 << 62)
+            fill.append(ks[:2])
+            batch.append(np.repeat(ks, rng.integers(10, 41)))
+        elif kind == 1:
+            batch.append(keys_in_bucket(rng, 40, cap, b, lo=1 << 40, hi=1 << 62))
+        elif kind == 2:
+            ks = keys_in_bucket(rng, 130, cap, b, lo=1 << 40, hi=1 << 62)
+            fill.append(ks[:125])
+            batch.append(np.concatenate([np.repeat(ks[125:], 10), np.repeat(ks[:3], 5)]))
+        else:
+            batch.append(keys_in_bucket(rng, 140, cap, b, lo=1 << 40, hi=1 << 62))
+    return np.concatenate(fill), np.concatenate(batch)
+
+
+@pytest.mark.parametrize("op", ["find_or_insert", "insert_or_assign", "insert_and_evict",
+                                "assign_scores"])
+@pytest.mark.parametrize("strategy", STRATS)
+def test_long_buckets_in_small_partitions(op, strategy):
+    rng = np.random.default_rng(380 + strategy)
+    cap, dim = 1 << 20, 4
+    p = Pair(cap, dim=dim, strategy=strategy)
+    p.set_global_epoch(6)
+    fill, hot = _long_bucket_batch(rng, p, cap, dim, strategy)
+    base = np.concatenate([fill, uniform_keys(rng, 1 << 17, exclude=fill)])
+    p.insert_or_assign(base, rand_vals(rng, base.size, dim),
+                       scores_for(strategy, rng, base.size), clock=10)
+    p.assert_same_state()
+    for r in range(2):
+        p.set_global_epoch(7 + r)
+        light = np.concatenate([rng.choice(base, 1500),
+                                uniform_keys(rng, 3000, exclude=np.concatenate([base, hot]))])
+        q = np.concatenate([hot, light])
+        q = q[rng.permutation(q.size)]
+        _run(p, op if r else "find_or_insert", rng, q, strategy, dim, clock=50 + r,
+             big=(r == 1))
+
+
+def test_long_buckets_accum():
+    """The same batches through accum_or_assign, which lists whole
+    partitions (its accumulations run in batch order, without a fold)."""
+    rng = np.random.default_rng(399)
+    cap, dim = 1 << 20, 4
+    for strategy in (O.LFU, O.CUSTOMIZED):
+        p = Pair(cap, dim=dim, strategy=strategy)
+        fill, hot = _long_bucket_batch(rng, p, cap, dim, strategy)
+        base = np.concatenate([fill, uniform_keys(rng, 1 << 16, exclude=fill)])
+        p.insert_or_assign(base, rand_vals(rng, base.size, dim),
+                           scores_for(strategy, rng, base.size), clock=10)
+        q = np.concatenate([hot, rng.choice(base, 1000), uniform_keys(rng, 2000, exclude=base)])
+        q = q[rng.permutation(q.size)]
+        flags = (rng.random(q.size) < 0.5).astype(np.uint8)
+        p.accum_or_assign(q, rng.uniform(-0.01, 0.01, (q.size, dim)).astype(np.float32), flags,
+                          scores_for(strategy, rng, q.size), clock=11)
+        p.assert_same_state()
