@@ -529,9 +529,21 @@ __device__ __forceinline__ uint64_t ev_slot(const ApplyArgs& a, uint64_t i, uint
 // this with the same i).  Restates, for one key, the reference kernels
 // insert_or_assign_kernel.h:76-303 (unique keys) and find_and_lock
 // (find_utils.h:94-227) with its callers (non-unique keys and accum).
-template <int OP, int U>
-__device__ __forceinline__ void apply_key_in(const TableView& t, Bucket16& S, const ApplyArgs& a,
-                                             uint64_t i, uint64_t k, uint64_t in) {
+// Row moves of one applied key, for callers that queue them instead of
+// running them in place (kRows = false): a read into the key's output row
+// (the slot's row, or the key's own input row) and a write of the slot (the
+// key's input row copied in, or its delta added).
+constexpr uint32_t kRdNone = 0, kRdSlot = 1, kRdSelf = 2, kRdFwd = 3;
+constexpr uint32_t kWrNone = 0, kWrCopy = 1, kWrAcc = 2;
+struct RowAct {
+  uint32_t rd, wr, pos;
+};
+
+template <int OP, int U, bool kRows = true>
+__device__ __forceinline__ RowAct apply_key_in(const TableView& t, Bucket16& S,
+                                               const ApplyArgs& a, uint64_t i, uint64_t k,
+                                               uint64_t in) {
+  RowAct act{kRdNone, kWrNone, 0};
   constexpr int SPL = 8;
   const uint32_t B = t.B;
   const uint32_t l = S.l;
@@ -562,7 +574,7 @@ __device__ __forceinline__ void apply_key_in(const TableView& t, Bucket16& S, co
     res = R_DUP;
     pos = best & 0xFFu;
   } else if (OP == OP_ASSIGN_SCORES) {
-    return;  // absent keys are a no-op
+    return act;  // absent keys are a no-op
   } else {
     // 2. First EMPTY slot (empty digest) in circular order from `start`.
     if (S.bsz < (int32_t)B) {
@@ -635,9 +647,9 @@ __device__ __forceinline__ void apply_key_in(const TableView& t, Bucket16& S, co
   const uint32_t R = t.row_bytes;
   gptr<const uint8_t> in_row = a.in_values ? G(a.in_values) + i * (uint64_t)R : nullptr;
   if (OP == OP_ACCUM_OR_ASSIGN) {
-    if (res == R_REFUSED) return;
+    if (res == R_REFUSED) return act;
     const bool is_accum = G(a.accum_flags)[i] != 0;
-    if ((is_accum && res != R_DUP) || (!is_accum && res == R_DUP)) return;
+    if ((is_accum && res != R_DUP) || (!is_accum && res == R_DUP)) return act;
   }
   if (res == R_REFUSED) {
     if (OP == OP_INSERT_AND_EVICT) {
@@ -646,9 +658,10 @@ __device__ __forceinline__ void apply_key_in(const TableView& t, Bucket16& S, co
         G(a.ev_keys)[j] = k;
         if (a.ev_scores) G(a.ev_scores)[j] = des;
       }
-      copy_units<U>(G(a.ev_values) + j * R, in_row, R, l, 16);
+      if (kRows) copy_units<U>(G(a.ev_values) + j * R, in_row, R, l, 16);
+      act.rd = kRdSelf;
     }
-    return;
+    return act;
   }
   gptr<uint8_t> trow = row_ptr(t, S.b, pos);
   const bool swapped = OP == OP_INSERT_AND_EVICT && res == R_EVICT;
@@ -659,7 +672,9 @@ __device__ __forceinline__ void apply_key_in(const TableView& t, Bucket16& S, co
       if (a.ev_scores) G(a.ev_scores)[j] = victim_score;
     }
     // victim row out and input row in, one pass
-    swap_units<U>(G(a.ev_values) + j * R, trow, in_row, R, l, 16);
+    if (kRows) swap_units<U>(G(a.ev_values) + j * R, trow, in_row, R, l, 16);
+    act.rd = kRdSlot;
+    act.wr = kWrCopy;
   }
   if (res == R_EMPTY || res == R_RECLAIMED) S.bsz++;
 
@@ -668,15 +683,20 @@ __device__ __forceinline__ void apply_key_in(const TableView& t, Bucket16& S, co
     // moves done above.
   } else if (res == R_DUP) {
     if (OP == OP_FIND_OR_INSERT) {
-      copy_units<U>(G(a.io_values) + i * (uint64_t)R, trow, R, l, 16);
+      if (kRows) copy_units<U>(G(a.io_values) + i * (uint64_t)R, trow, R, l, 16);
+      act.rd = kRdSlot;
     } else if (OP == OP_ACCUM_OR_ASSIGN) {
-      accum_row(trow, in_row, R, a.value_type, l, 16);
+      if (kRows) accum_row(trow, in_row, R, a.value_type, l, 16);
+      act.wr = kWrAcc;
     } else if (OP != OP_ASSIGN_SCORES) {
-      copy_units<U>(trow, in_row, R, l, 16);
+      if (kRows) copy_units<U>(trow, in_row, R, l, 16);
+      act.wr = kWrCopy;
     }
   } else {
-    copy_units<U>(trow, in_row, R, l, 16);
+    if (kRows) copy_units<U>(trow, in_row, R, l, 16);
+    act.wr = kWrCopy;
   }
+  act.pos = pos;
 
   const uint32_t owner = pos & 15u, jj = pos >> 4;
   if (l == owner) {
@@ -721,6 +741,7 @@ __device__ __forceinline__ void apply_key_in(const TableView& t, Bucket16& S, co
     if (OP == OP_FIND_OR_INSERT_PTR)
       G(a.slot_out)[i] = (S.base + pos + 1) | (res == R_DUP ? kSlotFound : 0ull);
   }
+  return act;
 }
 
 // apply_key_in with the key's input score loaded here.
@@ -3437,7 +3458,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
     // A bucket handed over takes a record and pool entries, counted here in
     // LDS; the block reserves them with one pair of atomics below.
     if (stop < c) {
-      hand = (atomicAdd(&s_nrec, 1u) << 16) | atomicAdd(&s_npool, c);
+      hand = (atomicAdd(&s_nrec, 1u) << 16) | atomicAdd(&s_npool, c - stop);
       hand_bk = bk;
     }
     if (bsz != s_bsz[bk]) {
@@ -3466,15 +3487,15 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
   }
   if (s_nrec) {  // uniform in the block
     lds_barrier();
-    // Hand-over records {bucket, keys, first key left, pool offset} and the
-    // bucket's keys in batch order, for k_apply_deferred.
+    // Hand-over records {bucket, keys left, 0, pool offset} and the keys
+    // left in batch order, for k_apply_deferred.
     if (hand != kNone) {
-      const uint32_t lo = s_off[hand_bk], hi = s_off[hand_bk + 1];
+      const uint32_t lo = s_off[hand_bk] + s_cnt[hand_bk], hi = s_off[hand_bk + 1];
       const uint32_t po = s_pbase + (hand & 0xFFFFu);
       gptr<uint32_t> rec = G(ps.drec) + 4 * (uint64_t)(s_rbase + (hand >> 16));
       rec[0] = (uint32_t)(part_b0 + hand_bk);
       rec[1] = hi - lo;
-      rec[2] = s_cnt[hand_bk];
+      rec[2] = 0;
       rec[3] = po;
       gptr<u64x2> pool = G(reinterpret_cast<u64x2*>(ps.dpool)) + po;
       for (uint32_t x = lo; x < hi; x++) {
@@ -3488,42 +3509,338 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
 
 }
 
-// One 16-lane group per bucket handed over by k_apply_fast, which applied
-// (and copied the rows of) the bucket's keys before `st`: the remaining keys
-// go through the eviction path, in batch order.
+// Element size of the accumulating value types (accum_row): 4 for f32 and
+// i32, 8 for i64 / u64, 0 for types that accumulate nothing.
+__host__ __device__ __forceinline__ uint32_t acc_elem(int vt) {
+  return (vt == 0 || vt == 8) ? 4u : (vt == 10 || vt == 11) ? 8u : 0u;
+}
+
+// Row moves of a deferred bucket, queued while its keys are applied and run
+// after its last key with every load of a round issued before the round's
+// first store.  Key q of the bucket (q < kDefKeys) has an entry held by lane
+// q & 15, in half q >> 4:
+//   ek: read kind (bits 0-1), write kind (bits 2-3), slot (bits 8-15);
+//   ex: batch index of the input row that the read forwards (kRdFwd, or the
+//       key itself for kRdSelf) or that the write copies or adds;
+//   ei: the key's batch index (its output row).
+// All moves that touch one slot sit in one entry, the slot's owner: its read
+// of the slot's row as the queue found it, then the slot's last write.  The
+// other entries read input rows, which no move writes, and write their own
+// output rows; so the entries are independent and run in any order.  A move
+// the queue cannot hold that way (a write after two reads of the slot, or
+// after a read by another key that reads it again; an addition after any
+// earlier move on the slot) runs the queue first.
+constexpr uint32_t kDefKeys = 32;
+constexpr uint32_t kSsOwner = 0x3F;   // slot state: owner entry + 1
+constexpr uint32_t kSsWrite = 0x40;   // the owner writes the slot
+constexpr uint32_t kSsMulti = 0x80;   // two or more entries read the slot
+
+struct DeferQ {
+  uint32_t ek0, ek1, ex0, ex1, ei0, ei1;
+  uint32_t ss0, ss1;  // state of slot l + 16j in byte j (ss0: j < 4)
+};
+
+__device__ __forceinline__ uint32_t dq_get(uint32_t v0, uint32_t v1, uint32_t q) {
+  return (uint32_t)__shfl((int)(q < 16 ? v0 : v1), (int)(q & 15), 16);
+}
+__device__ __forceinline__ void dq_set(uint32_t& v0, uint32_t& v1, uint32_t l, uint32_t q,
+                                       uint32_t v) {
+  if (l == (q & 15)) {
+    if (q < 16) v0 = v;
+    else v1 = v;
+  }
+}
+__device__ __forceinline__ uint32_t ss_get(const DeferQ& Q, uint32_t pos) {
+  const uint32_t j = pos >> 4;
+  const uint32_t w = (uint32_t)__shfl((int)(j < 4 ? Q.ss0 : Q.ss1), (int)(pos & 15), 16);
+  return (w >> (8 * (j & 3))) & 0xFFu;
+}
+__device__ __forceinline__ void ss_set(DeferQ& Q, uint32_t l, uint32_t pos, uint32_t v) {
+  if (l != (pos & 15)) return;
+  const uint32_t j = pos >> 4, sh = 8 * (j & 3);
+  const uint32_t m = ~(0xFFu << sh);
+  if (j < 4) Q.ss0 = (Q.ss0 & m) | (v << sh);
+  else Q.ss1 = (Q.ss1 & m) | (v << sh);
+}
+
+// Runs the queued moves of entries q < nq (all 16 lanes of the group), two
+// entries per round, and empties the queue.
 template <int OP, int U>
-__global__ __launch_bounds__(kBlock) void k_apply_deferred(TableView t, ApplyArgs a,
-                                                           PartScratch ps) {
+__device__ __forceinline__ void defer_run(const TableView& t, const ApplyArgs& a, uint64_t b,
+                                       uint32_t l, DeferQ& Q, uint32_t nq) {
+  using T = typename UnitT<U>::T;
+  const uint64_t R = t.row_bytes;
+  const uint32_t units = t.row_bytes / U;
+  const uint32_t gsh = threadIdx.x & 48;  // the group's first lane in the wave
+  const uint64_t b0 = __ballot(Q.ek0 != 0 && l < nq);
+  const uint64_t b1 = __ballot(Q.ek1 != 0 && l + 16 < nq);
+  uint32_t mk = (uint32_t)((b0 >> gsh) & 0xFFFFu) | ((uint32_t)((b1 >> gsh) & 0xFFFFu) << 16);
+  const uint64_t in_base = (uint64_t)(uintptr_t)a.in_values;
+  const uint64_t out_base =
+      (uint64_t)(uintptr_t)(OP == OP_INSERT_AND_EVICT ? a.ev_values : a.io_values);
+  const bool acc_any = acc_elem(a.value_type) != 0;
+  while (mk) {  // uniform in the group
+    uint64_t src[4], dst[4];
+    bool acc[2];
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+      src[2 * e] = src[2 * e + 1] = dst[2 * e] = dst[2 * e + 1] = 0;
+      acc[e] = false;
+      if (!mk) continue;
+      const uint32_t q = (uint32_t)__builtin_ctz(mk);
+      mk &= mk - 1;
+      const uint32_t ek = dq_get(Q.ek0, Q.ek1, q), ex = dq_get(Q.ex0, Q.ex1, q),
+                     ei = dq_get(Q.ei0, Q.ei1, q);
+      const uint32_t rd = ek & 3u, wr = (ek >> 2) & 3u, pos = (ek >> 8) & 0xFFu;
+      const uint64_t slot = (uint64_t)(uintptr_t)row_ptr(t, b, pos);
+      if (rd != kRdNone) {
+        src[2 * e] = rd == kRdSlot ? slot : in_base + (uint64_t)ex * R;
+        dst[2 * e] = out_base + (uint64_t)ei * R;
+      }
+      if (wr == kWrCopy) {
+        src[2 * e + 1] = in_base + (uint64_t)ex * R;
+        dst[2 * e + 1] = slot;
+      } else if (wr == kWrAcc && acc_any) {
+        src[2 * e] = slot;  // the row (no read entry holds an addition)
+        src[2 * e + 1] = in_base + (uint64_t)ex * R;  // the delta
+        dst[2 * e + 1] = slot;
+        acc[e] = true;
+      }
+    }
+    gptr<const T> sp[4];
+    gptr<T> dp[4];
+#pragma unroll
+    for (int x = 0; x < 4; x++) {
+      sp[x] = G<const T>((uintptr_t)src[x]);
+      dp[x] = G<T>((uintptr_t)dst[x]);
+    }
+    for (uint32_t u0 = l; u0 < units; u0 += 32) {
+      T v[4][2];
+#pragma unroll
+      for (int x = 0; x < 4; x++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          const uint32_t u = u0 + 16 * h;
+          if (src[x] && u < units) v[x][h] = __builtin_nontemporal_load(&sp[x][u]);
+        }
+#pragma unroll
+      for (int e = 0; e < 2; e++)
+        if (acc[e])
+#pragma unroll
+          for (int h = 0; h < 2; h++)
+            if (u0 + 16 * h < units)
+              v[2 * e + 1][h] = add_unit(v[2 * e][h], v[2 * e + 1][h], a.value_type);
+#pragma unroll
+      for (int x = 0; x < 4; x++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          const uint32_t u = u0 + 16 * h;
+          if (dst[x] && u < units) __builtin_nontemporal_store(v[x][h], &dp[x][u]);
+        }
+    }
+  }
+  Q.ek0 = Q.ek1 = 0;
+  Q.ss0 = Q.ss1 = 0;
+}
+
+// defer_run for the queue cut short inside a bucket (rare: a move that
+// cannot join it), one entry and one unit per lane at a time, so that it
+// adds few registers to the bucket state held across it.
+template <int OP, int U>
+__device__ __forceinline__ void defer_run_narrow(const TableView& t, const ApplyArgs& a,
+                                                 uint64_t b, uint32_t l, DeferQ& Q,
+                                                 uint32_t nq) {
+  using T = typename UnitT<U>::T;
+  const uint64_t R = t.row_bytes;
+  const uint32_t units = t.row_bytes / U;
+  const uint64_t in_base = (uint64_t)(uintptr_t)a.in_values;
+  const uint64_t out_base =
+      (uint64_t)(uintptr_t)(OP == OP_INSERT_AND_EVICT ? a.ev_values : a.io_values);
+  const bool acc_any = acc_elem(a.value_type) != 0;
+  for (uint32_t q = 0; q < nq; q++) {  // uniform in the group
+    const uint32_t ek = dq_get(Q.ek0, Q.ek1, q);
+    if (!ek) continue;
+    const uint32_t ex = dq_get(Q.ex0, Q.ex1, q), ei = dq_get(Q.ei0, Q.ei1, q);
+    const uint32_t rd = ek & 3u, wr = (ek >> 2) & 3u, pos = (ek >> 8) & 0xFFu;
+    const uint64_t slot = (uint64_t)(uintptr_t)row_ptr(t, b, pos);
+    uint64_t sa = 0, da = 0, sb = 0, db = 0;
+    bool acc = false;
+    if (rd != kRdNone) {
+      sa = rd == kRdSlot ? slot : in_base + (uint64_t)ex * R;
+      da = out_base + (uint64_t)ei * R;
+    }
+    if (wr == kWrCopy) {
+      sb = in_base + (uint64_t)ex * R;
+      db = slot;
+    } else if (wr == kWrAcc && acc_any) {
+      sa = slot;
+      sb = in_base + (uint64_t)ex * R;
+      db = slot;
+      acc = true;
+    }
+    for (uint32_t u = l; u < units; u += 16) {
+      T va{}, vb{};
+      if (sa) va = __builtin_nontemporal_load(&G<const T>((uintptr_t)sa)[u]);
+      if (sb) vb = __builtin_nontemporal_load(&G<const T>((uintptr_t)sb)[u]);
+      if (acc) vb = add_unit(va, vb, a.value_type);
+      if (da) __builtin_nontemporal_store(va, &G<T>((uintptr_t)da)[u]);
+      if (db) __builtin_nontemporal_store(vb, &G<T>((uintptr_t)db)[u]);
+    }
+  }
+  Q.ek0 = Q.ek1 = 0;
+  Q.ss0 = Q.ss1 = 0;
+}
+
+// True when the row moves of `act` cannot join the queue as it stands (the
+// queue runs first, then they join the emptied queue).
+__device__ __forceinline__ bool defer_conflict(const DeferQ& Q, const RowAct& act) {
+  if (act.wr == kWrNone) return false;  // reads always join
+  const uint32_t s = ss_get(Q, act.pos);
+  if (!(s & kSsOwner)) return false;
+  if (act.wr == kWrAcc) return true;
+  return !(s & kSsWrite) && ((s & kSsMulti) || act.rd == kRdSlot);
+}
+
+// Queues the row moves of entry e (batch index i) that apply_key_in decided
+// without running them (defer_conflict(Q, act) is false).
+__device__ __forceinline__ void defer_note(uint32_t l, DeferQ& Q, uint32_t e, uint32_t i,
+                                           const RowAct& act) {
+  if (act.rd == kRdNone && act.wr == kWrNone) return;  // uniform in the group
+  const bool on_slot = act.rd == kRdSlot || act.wr != kWrNone;
+  uint32_t s = on_slot ? ss_get(Q, act.pos) : 0u;
+  uint32_t own = s & kSsOwner;
+  uint32_t ek = act.pos << 8, ex = 0;
+  if (act.rd == kRdSelf) {
+    ek |= kRdFwd;
+    ex = i;
+  } else if (act.rd == kRdSlot) {
+    if (s & kSsWrite) {
+      // The slot holds the owner's queued input row: forward that row.
+      ek |= kRdFwd;
+      ex = dq_get(Q.ex0, Q.ex1, own - 1);
+    } else {
+      ek |= kRdSlot;
+      if (own) {
+        s |= kSsMulti;
+      } else {
+        own = e + 1;
+        s = own;
+      }
+    }
+  }
+  if (act.wr != kWrNone) {
+    if (own && own != e + 1) {
+      // The owner's entry carries the slot's write: this key's input row
+      // replaces whatever it queued for the slot.
+      const uint32_t o = own - 1;
+      const uint32_t oek = dq_get(Q.ek0, Q.ek1, o);
+      dq_set(Q.ek0, Q.ek1, l, o, (oek & ~0xCu) | (kWrCopy << 2));
+      dq_set(Q.ex0, Q.ex1, l, o, i);
+      s |= kSsWrite;
+    } else {
+      ek |= act.wr << 2;
+      ex = i;
+      s = (e + 1) | kSsWrite;
+    }
+  }
+  dq_set(Q.ek0, Q.ek1, l, e, ek);
+  dq_set(Q.ex0, Q.ex1, l, e, ex);
+  dq_set(Q.ei0, Q.ei1, l, e, i);
+  if (on_slot) ss_set(Q, l, act.pos, s);
+}
+
+// One 16-lane group per bucket handed over by k_apply_fast, which applied
+// (and copied the rows of) the bucket's earlier keys: the keys left go
+// through the eviction path, in batch order.  With kQueue the row moves are
+// queued and run after the bucket's last key (defer_run; in segments of at
+// most kDefKeys keys, cut early where a move cannot join the queue), and the
+// next record and its keys load while a bucket is applied, so a bucket costs
+// about two memory round trips instead of one per key.  Without kQueue
+// (assign_scores, which moves no rows) each key's moves run in place.
+template <int OP, int U, bool kQueue>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 4))) void
+k_apply_deferred(TableView t, ApplyArgs a, PartScratch ps) {
   const uint32_t nrec = *(volatile uint32_t*)ps.dctr;
   const uint32_t gl = threadIdx.x & 15;
   const uint64_t ngroups = (uint64_t)gridDim.x * (kBlock / 16);
+  uint64_t r = ((uint64_t)blockIdx.x * kBlock + threadIdx.x) >> 4;
+  if (r >= nrec) return;  // uniform in the group
+  const bool has_in = a.in_scores != nullptr;
   gptr<const u64x2> pool = G(reinterpret_cast<const u64x2*>(ps.dpool));
-  for (uint64_t r = ((uint64_t)blockIdx.x * kBlock + threadIdx.x) >> 4; r < nrec;
-       r += ngroups) {
-    gptr<const uint32_t> rec = G(ps.drec) + 4 * r;
-    const uint64_t b = rec[0];
-    const uint32_t c = rec[1], st = rec[2], po = rec[3];
-    // The first 16 keys left, one per lane, and their input scores, load
-    // beside the bucket instead of one dependent pair per step.
-    u64x2 mine;
-    mine.x = 0;
-    mine.y = 0;
-    if (st + gl < c) mine = pool[po + st + gl];
+  gptr<const uint32_t> drec = G(ps.drec);
+  uint64_t b = drec[4 * r];
+  uint32_t c = drec[4 * r + 1], po = drec[4 * r + 3];
+  u64x2 mine;
+  mine.x = 0;
+  mine.y = 0;
+  if (gl < c) mine = pool[po + gl];
+  uint64_t mine_in = (gl < c && has_in) ? G(a.in_scores)[mine.y] : 0;
+  while (true) {
     Bucket16 S;
     bucket_load(t, S, b, gl);
-    const uint64_t mine_in = (st + gl < c && a.in_scores) ? G(a.in_scores)[mine.y] : 0;
-    for (uint32_t step = st; step < c; step++) {
-      const uint32_t j = step - st;  // uniform in the group
-      if (j < 16) {
-        const uint64_t k = shfl_u64(mine.x, (int)j, 16);
-        const uint64_t i = shfl_u64(mine.y, (int)j, 16);
-        apply_key_in<OP, U>(t, S, a, i, k, shfl_u64(mine_in, (int)j, 16));
-      } else {
-        const u64x2 v = pool[po + step];
-        apply_key<OP, U>(t, S, a, v.y, v.x);
+    const uint64_t rn = r + ngroups;
+    uint64_t nb = 0;
+    uint32_t nc = 0, npo = 0;
+    if (rn < nrec) {
+      nb = drec[4 * rn];
+      nc = drec[4 * rn + 1];
+      npo = drec[4 * rn + 3];
+    }
+    u64x2 nmine;
+    nmine.x = 0;
+    nmine.y = 0;
+    if (gl < nc) nmine = pool[npo + gl];
+    uint64_t nin = 0;
+    if (kQueue) {
+      DeferQ Q;
+      Q.ek0 = Q.ek1 = Q.ex0 = Q.ex1 = Q.ei0 = Q.ei1 = Q.ss0 = Q.ss1 = 0;
+      uint32_t seg0 = 0;  // first key of the queue's segment
+      for (uint32_t q = 0; q < c; q++) {  // uniform in the group
+        uint64_t k, i, in;
+        if (q < 16) {
+          k = shfl_u64(mine.x, (int)q, 16);
+          i = shfl_u64(mine.y, (int)q, 16);
+          in = shfl_u64(mine_in, (int)q, 16);
+        } else {
+          const u64x2 v = pool[po + q];
+          k = v.x;
+          i = v.y;
+          in = has_in ? G(a.in_scores)[i] : 0;
+        }
+        const RowAct act = apply_key_in<OP, U, false>(t, S, a, i, k, in);
+        if (q - seg0 == kDefKeys || defer_conflict(Q, act)) {
+          defer_run_narrow<OP, U>(t, a, b, gl, Q, q - seg0);
+          seg0 = q;
+        }
+        defer_note(gl, Q, q - seg0, (uint32_t)i, act);
       }
+      nin = (gl < nc && has_in) ? G(a.in_scores)[nmine.y] : 0;
+      defer_run<OP, U>(t, a, b, gl, Q, c - seg0);
+    } else {
+      for (uint32_t q = 0; q < c; q++) {
+        uint64_t k, i, in;
+        if (q < 16) {
+          k = shfl_u64(mine.x, (int)q, 16);
+          i = shfl_u64(mine.y, (int)q, 16);
+          in = shfl_u64(mine_in, (int)q, 16);
+        } else {
+          const u64x2 v = pool[po + q];
+          k = v.x;
+          i = v.y;
+          in = has_in ? G(a.in_scores)[i] : 0;
+        }
+        apply_key_in<OP, U, true>(t, S, a, i, k, in);
+      }
+      nin = (gl < nc && has_in) ? G(a.in_scores)[nmine.y] : 0;
     }
     bucket_finish(t, S);
+    if (rn >= nrec) break;
+    r = rn;
+    b = nb;
+    c = nc;
+    po = npo;
+    mine = nmine;
+    mine_in = nin;
   }
 }
 
@@ -4256,7 +4573,11 @@ static void apply_part_op(const TableView& t, const ApplyArgs& a, const PartScra
   const dim3 gb(grid_for(a.n / kBigTile + kBigMax, 1, 1024));
 #define HKV_PART_U(UU)                                                                       \
   hipLaunchKernelGGL((k_apply_fast<OP, UU>), g, b, 0, s, t, a, ps);                          \
-  hipLaunchKernelGGL((k_apply_deferred<OP, UU>), gd, b, 0, s, t, a, ps);                     \
+  if (OP != OP_ASSIGN_SCORES && (OP != OP_INSERT_AND_EVICT || a.ev_bits) &&                  \
+      (OP != OP_ACCUM_OR_ASSIGN || UU >= acc_elem(a.value_type)))                            \
+    hipLaunchKernelGGL((k_apply_deferred<OP, UU, OP != OP_ASSIGN_SCORES>), gd, b, 0, s, t, a, ps); \
+  else                                                                                       \
+    hipLaunchKernelGGL((k_apply_deferred<OP, UU, false>), gd, b, 0, s, t, a, ps);              \
   if (ps.big) {                                                                              \
     hipLaunchKernelGGL(k_big_clear, dim3(kBigMax), b, 0, s, ps);                              \
     hipLaunchKernelGGL(k_big_count, gb, b, 0, s, t, ps);                                     \
