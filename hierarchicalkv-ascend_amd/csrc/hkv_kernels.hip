@@ -398,8 +398,7 @@ enum Outcome : uint32_t { R_DUP = 1, R_EMPTY = 2, R_RECLAIMED = 3, R_EVICT = 4, 
 // evicting key scans no memory.  Only the owner lane reads or writes a slot,
 // which keeps the registers current; writes go through to the table.
 struct Bucket16 {
-  uint64_t b;
-  uint64_t base;  // b * B
+  uint32_t b;  // bucket (bucket counts stay below 2^32)
   uint32_t l;
   uint32_t dg0, dg1;  // digest of slot l+16j in byte j (dg0: j<4, dg1: j>=4)
   int32_t bsz, bsz0;
@@ -437,21 +436,26 @@ __device__ __forceinline__ void dg_set(Bucket16& S, uint32_t j, uint32_t d) {
 
 __device__ __forceinline__ void bucket_load(const TableView& t, Bucket16& S, uint64_t b,
                                             uint32_t l) {
-  S.b = b;
-  S.base = b * (uint64_t)t.B;
+  S.b = (uint32_t)b;
   S.l = l;
-  gptr<const uint8_t> dg = G(t.digests) + S.base + l;
+  const uint64_t base = b * (uint64_t)t.B;
+  gptr<const uint8_t> dg = G(t.digests) + base + l;
   S.dg0 = (uint32_t)dg[0] | ((uint32_t)dg[16] << 8) | ((uint32_t)dg[32] << 16) |
           ((uint32_t)dg[48] << 24);
   S.dg1 = (uint32_t)dg[64] | ((uint32_t)dg[80] << 8) | ((uint32_t)dg[96] << 16) |
           ((uint32_t)dg[112] << 24);
 #pragma unroll
   for (uint32_t j = 0; j < 8; j++) {
-    const u64x2 r = slot_load(t, S.base + l + 16 * j);
+    const u64x2 r = slot_load(t, base + l + 16 * j);
     S.key[j] = r.x;
     S.score[j] = r.y;
   }
   S.bsz = S.bsz0 = G(t.bsize)[b];
+}
+
+// First slot of the bucket a group holds.
+__device__ __forceinline__ uint64_t sbase(const TableView& t, const Bucket16& S) {
+  return (uint64_t)S.b * t.B;
 }
 
 // Group-wide minimum of (score, rank) carrying the slot and its key.
@@ -721,25 +725,25 @@ __device__ __forceinline__ RowAct apply_key_in(const TableView& t, Bucket16& S,
     const uint64_t wk = lk ? kLockedKey : k;
     if (res == R_DUP) {
       if (w) {
-        slot_score(t, S.base + pos) = ns;
+        slot_score(t, sbase(t, S) + pos) = ns;
         rec_set(S.score, jj, ns);
       }
       if (lk) {
-        slot_key(t, S.base + pos) = kLockedKey;
+        slot_key(t, sbase(t, S) + pos) = kLockedKey;
         rec_set(S.key, jj, kLockedKey);
       }
     } else if (w) {
-      slot_store(t, S.base + pos, wk, ns);
-      G(t.digests)[S.base + pos] = (uint8_t)d;
+      slot_store(t, sbase(t, S) + pos, wk, ns);
+      G(t.digests)[sbase(t, S) + pos] = (uint8_t)d;
       dg_set(S, jj, d);
       rec_set(S.key, jj, wk);
       rec_set(S.score, jj, ns);
     } else {
-      slot_key(t, S.base + pos) = wk;
+      slot_key(t, sbase(t, S) + pos) = wk;
       rec_set(S.key, jj, wk);
     }
     if (OP == OP_FIND_OR_INSERT_PTR)
-      G(a.slot_out)[i] = (S.base + pos + 1) | (res == R_DUP ? kSlotFound : 0ull);
+      G(a.slot_out)[i] = (sbase(t, S) + pos + 1) | (res == R_DUP ? kSlotFound : 0ull);
   }
   return act;
 }
@@ -1816,10 +1820,10 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
               const uint64_t ns = heavy_score<OP>(a.sc, has_in, is_new, old, msum[q], in_last);
               if (is_new) {
                 const uint64_t k = mkey[q];
-                slot_store(t, S.base + pos, k, ns);
-                G(t.digests)[S.base + pos] = (uint8_t)key_digest(murmur3(k));
+                slot_store(t, sbase(t, S) + pos, k, ns);
+                G(t.digests)[sbase(t, S) + pos] = (uint8_t)key_digest(murmur3(k));
               } else {
-                slot_score(t, S.base + pos) = ns;
+                slot_score(t, sbase(t, S) + pos) = ns;
               }
             }
             nadd += is_new ? 1 : 0;
@@ -2237,8 +2241,8 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
 // three times: entries per bucket (H0), the heavy-bucket fold (H1) and the
 // per-occurrence row work (H3).  k_apply_fast lists such partitions in
 // big slots, and these passes run over the whole GPU instead, with each
-// partition's counts and key map in its slot in global memory:
-//   k_big_clear  resets the listed slots;
+// partition's counts and key map in its slot in global memory (the block
+// of k_apply_fast that lists a partition resets its slot):
 //   k_big_count  adds up entries per bucket;
 //   k_big_fold   folds the heavy buckets' entries into the key map (first
 //                and last batch index and score sum per key: associative,
@@ -2294,11 +2298,8 @@ __device__ __forceinline__ uint32_t big_slot_of(const uint32_t* s_pre, uint32_t 
   return lo;
 }
 
-__global__ __launch_bounds__(kBlock) void k_big_clear(PartScratch ps) {
-  const uint32_t s = blockIdx.x, tid = threadIdx.x;
-  const uint32_t nb = *(volatile uint32_t*)&ps.dctr[4];
-  if (s >= nb || s >= kBigMax) return;
-  BigSlot& S = ps.big[s];
+// Resets one slot of big-partition state (all kBlock threads of a block).
+__device__ __forceinline__ void big_slot_reset(BigSlot& S, uint32_t tid) {
   S.tot[tid] = 0;
   for (uint32_t q = tid; q < kBigMapCap; q += kBlock) {
     S.mkey[q] = kEmptyKey;
@@ -3014,13 +3015,22 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
   const uint32_t p = blockIdx.x;
   const uint32_t base_e = ps.pinfo[2 * p], m_all = ps.pinfo[2 * p + 1];
   if (m_all > kFastLds) {
+    // k_apply_part takes the partition; a big one also gets a slot of
+    // big-partition state, which this block resets for k_big_count.
+    __shared__ uint32_t s_slot_big;
     if (tid == 0) {
-      ps.plist[atomicAdd(&ps.dctr[2], 1u)] = p;  // k_apply_part takes it
+      ps.plist[atomicAdd(&ps.dctr[2], 1u)] = p;
+      s_slot_big = kNone;
       if (ps.big && m_all > kBigPart) {
         const uint32_t sl = atomicAdd(&ps.dctr[4], 1u);
-        if (sl < kBigMax) ps.big_part[sl] = p;
+        if (sl < kBigMax) {
+          ps.big_part[sl] = p;
+          s_slot_big = sl;
+        }
       }
     }
+    __syncthreads();
+    if (s_slot_big != kNone) big_slot_reset(ps.big[s_slot_big], tid);
     return;
   }
   if (m_all == 0) return;
@@ -3530,25 +3540,21 @@ __host__ __device__ __forceinline__ uint32_t acc_elem(int vt) {
 // the queue cannot hold that way (a write after two reads of the slot, or
 // after a read by another key that reads it again; an addition after any
 // earlier move on the slot) runs the queue first.
-constexpr uint32_t kDefKeys = 32;
+constexpr uint32_t kDefKeys = 16;
 constexpr uint32_t kSsOwner = 0x3F;   // slot state: owner entry + 1
 constexpr uint32_t kSsWrite = 0x40;   // the owner writes the slot
 constexpr uint32_t kSsMulti = 0x80;   // two or more entries read the slot
 
 struct DeferQ {
-  uint32_t ek0, ek1, ex0, ex1, ei0, ei1;
-  uint32_t ss0, ss1;  // state of slot l + 16j in byte j (ss0: j < 4)
+  uint32_t ek, ex, ei;  // entry q held by lane q
+  uint32_t ss0, ss1;    // state of slot l + 16j in byte j (ss0: j < 4)
 };
 
-__device__ __forceinline__ uint32_t dq_get(uint32_t v0, uint32_t v1, uint32_t q) {
-  return (uint32_t)__shfl((int)(q < 16 ? v0 : v1), (int)(q & 15), 16);
+__device__ __forceinline__ uint32_t dq_get(uint32_t v, uint32_t q) {
+  return (uint32_t)__shfl((int)v, (int)q, 16);
 }
-__device__ __forceinline__ void dq_set(uint32_t& v0, uint32_t& v1, uint32_t l, uint32_t q,
-                                       uint32_t v) {
-  if (l == (q & 15)) {
-    if (q < 16) v0 = v;
-    else v1 = v;
-  }
+__device__ __forceinline__ void dq_set(uint32_t& v, uint32_t l, uint32_t q, uint32_t v_new) {
+  if (l == q) v = v_new;
 }
 __device__ __forceinline__ uint32_t ss_get(const DeferQ& Q, uint32_t pos) {
   const uint32_t j = pos >> 4;
@@ -3572,9 +3578,8 @@ __device__ __forceinline__ void defer_run(const TableView& t, const ApplyArgs& a
   const uint64_t R = t.row_bytes;
   const uint32_t units = t.row_bytes / U;
   const uint32_t gsh = threadIdx.x & 48;  // the group's first lane in the wave
-  const uint64_t b0 = __ballot(Q.ek0 != 0 && l < nq);
-  const uint64_t b1 = __ballot(Q.ek1 != 0 && l + 16 < nq);
-  uint32_t mk = (uint32_t)((b0 >> gsh) & 0xFFFFu) | ((uint32_t)((b1 >> gsh) & 0xFFFFu) << 16);
+  const uint64_t b0 = __ballot(Q.ek != 0 && l < nq);
+  uint32_t mk = (uint32_t)((b0 >> gsh) & 0xFFFFu);
   const uint64_t in_base = (uint64_t)(uintptr_t)a.in_values;
   const uint64_t out_base =
       (uint64_t)(uintptr_t)(OP == OP_INSERT_AND_EVICT ? a.ev_values : a.io_values);
@@ -3589,8 +3594,8 @@ __device__ __forceinline__ void defer_run(const TableView& t, const ApplyArgs& a
       if (!mk) continue;
       const uint32_t q = (uint32_t)__builtin_ctz(mk);
       mk &= mk - 1;
-      const uint32_t ek = dq_get(Q.ek0, Q.ek1, q), ex = dq_get(Q.ex0, Q.ex1, q),
-                     ei = dq_get(Q.ei0, Q.ei1, q);
+      const uint32_t ek = dq_get(Q.ek, q), ex = dq_get(Q.ex, q),
+                     ei = dq_get(Q.ei, q);
       const uint32_t rd = ek & 3u, wr = (ek >> 2) & 3u, pos = (ek >> 8) & 0xFFu;
       const uint64_t slot = (uint64_t)(uintptr_t)row_ptr(t, b, pos);
       if (rd != kRdNone) {
@@ -3639,7 +3644,7 @@ __device__ __forceinline__ void defer_run(const TableView& t, const ApplyArgs& a
         }
     }
   }
-  Q.ek0 = Q.ek1 = 0;
+  Q.ek = 0;
   Q.ss0 = Q.ss1 = 0;
 }
 
@@ -3658,9 +3663,9 @@ __device__ __forceinline__ void defer_run_narrow(const TableView& t, const Apply
       (uint64_t)(uintptr_t)(OP == OP_INSERT_AND_EVICT ? a.ev_values : a.io_values);
   const bool acc_any = acc_elem(a.value_type) != 0;
   for (uint32_t q = 0; q < nq; q++) {  // uniform in the group
-    const uint32_t ek = dq_get(Q.ek0, Q.ek1, q);
+    const uint32_t ek = dq_get(Q.ek, q);
     if (!ek) continue;
-    const uint32_t ex = dq_get(Q.ex0, Q.ex1, q), ei = dq_get(Q.ei0, Q.ei1, q);
+    const uint32_t ex = dq_get(Q.ex, q), ei = dq_get(Q.ei, q);
     const uint32_t rd = ek & 3u, wr = (ek >> 2) & 3u, pos = (ek >> 8) & 0xFFu;
     const uint64_t slot = (uint64_t)(uintptr_t)row_ptr(t, b, pos);
     uint64_t sa = 0, da = 0, sb = 0, db = 0;
@@ -3687,7 +3692,7 @@ __device__ __forceinline__ void defer_run_narrow(const TableView& t, const Apply
       if (db) __builtin_nontemporal_store(vb, &G<T>((uintptr_t)db)[u]);
     }
   }
-  Q.ek0 = Q.ek1 = 0;
+  Q.ek = 0;
   Q.ss0 = Q.ss1 = 0;
 }
 
@@ -3717,7 +3722,7 @@ __device__ __forceinline__ void defer_note(uint32_t l, DeferQ& Q, uint32_t e, ui
     if (s & kSsWrite) {
       // The slot holds the owner's queued input row: forward that row.
       ek |= kRdFwd;
-      ex = dq_get(Q.ex0, Q.ex1, own - 1);
+      ex = dq_get(Q.ex, own - 1);
     } else {
       ek |= kRdSlot;
       if (own) {
@@ -3733,9 +3738,9 @@ __device__ __forceinline__ void defer_note(uint32_t l, DeferQ& Q, uint32_t e, ui
       // The owner's entry carries the slot's write: this key's input row
       // replaces whatever it queued for the slot.
       const uint32_t o = own - 1;
-      const uint32_t oek = dq_get(Q.ek0, Q.ek1, o);
-      dq_set(Q.ek0, Q.ek1, l, o, (oek & ~0xCu) | (kWrCopy << 2));
-      dq_set(Q.ex0, Q.ex1, l, o, i);
+      const uint32_t oek = dq_get(Q.ek, o);
+      dq_set(Q.ek, l, o, (oek & ~0xCu) | (kWrCopy << 2));
+      dq_set(Q.ex, l, o, i);
       s |= kSsWrite;
     } else {
       ek |= act.wr << 2;
@@ -3743,23 +3748,59 @@ __device__ __forceinline__ void defer_note(uint32_t l, DeferQ& Q, uint32_t e, ui
       s = (e + 1) | kSsWrite;
     }
   }
-  dq_set(Q.ek0, Q.ek1, l, e, ek);
-  dq_set(Q.ex0, Q.ex1, l, e, ex);
-  dq_set(Q.ei0, Q.ei1, l, e, i);
+  dq_set(Q.ek, l, e, ek);
+  dq_set(Q.ex, l, e, ex);
+  dq_set(Q.ei, l, e, i);
   if (on_slot) ss_set(Q, l, act.pos, s);
 }
 
 // One 16-lane group per bucket handed over by k_apply_fast, which applied
 // (and copied the rows of) the bucket's earlier keys: the keys left go
-// through the eviction path, in batch order.  With kQueue the row moves are
-// queued and run after the bucket's last key (defer_run; in segments of at
-// most kDefKeys keys, cut early where a move cannot join the queue), and the
-// next record and its keys load while a bucket is applied, so a bucket costs
-// about two memory round trips instead of one per key.  Without kQueue
-// (assign_scores, which moves no rows) each key's moves run in place.
-template <int OP, int U, bool kQueue>
+// through the eviction path, in batch order, each key's row moves in place.
+template <int OP, int U>
+__global__ __launch_bounds__(kBlock) void k_apply_deferred(TableView t, ApplyArgs a,
+                                                           PartScratch ps) {
+  const uint32_t nrec = *(volatile uint32_t*)ps.dctr;
+  const uint32_t gl = threadIdx.x & 15;
+  const uint64_t ngroups = (uint64_t)gridDim.x * (kBlock / 16);
+  gptr<const u64x2> pool = G(reinterpret_cast<const u64x2*>(ps.dpool));
+  for (uint64_t r = ((uint64_t)blockIdx.x * kBlock + threadIdx.x) >> 4; r < nrec;
+       r += ngroups) {
+    gptr<const uint32_t> rec = G(ps.drec) + 4 * r;
+    const uint64_t b = rec[0];
+    const uint32_t c = rec[1], po = rec[3];
+    // The first 16 keys, one per lane, and their input scores, load beside
+    // the bucket instead of one dependent pair per step.
+    u64x2 mine;
+    mine.x = 0;
+    mine.y = 0;
+    if (gl < c) mine = pool[po + gl];
+    Bucket16 S;
+    bucket_load(t, S, b, gl);
+    const uint64_t mine_in = (gl < c && a.in_scores) ? G(a.in_scores)[mine.y] : 0;
+    for (uint32_t q = 0; q < c; q++) {  // uniform in the group
+      if (q < 16) {
+        const uint64_t k = shfl_u64(mine.x, (int)q, 16);
+        const uint64_t i = shfl_u64(mine.y, (int)q, 16);
+        apply_key_in<OP, U>(t, S, a, i, k, shfl_u64(mine_in, (int)q, 16));
+      } else {
+        const u64x2 v = pool[po + q];
+        apply_key<OP, U>(t, S, a, v.y, v.x);
+      }
+    }
+    bucket_finish(t, S);
+  }
+}
+
+// k_apply_deferred for insert_and_evict and accum_or_assign, whose
+// handed-over buckets carry the most row traffic: the row moves are queued
+// and run after the bucket's last key (defer_run; in segments of at most
+// kDefKeys keys, cut early where a move cannot join the queue), and the next
+// record and its keys load while a bucket is applied, so a bucket costs
+// about two memory round trips instead of one per key.
+template <int OP, int U>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 4))) void
-k_apply_deferred(TableView t, ApplyArgs a, PartScratch ps) {
+k_apply_deferred_q(TableView t, ApplyArgs a, PartScratch ps) {
   const uint32_t nrec = *(volatile uint32_t*)ps.dctr;
   const uint32_t gl = threadIdx.x & 15;
   const uint64_t ngroups = (uint64_t)gridDim.x * (kBlock / 16);
@@ -3770,11 +3811,14 @@ k_apply_deferred(TableView t, ApplyArgs a, PartScratch ps) {
   gptr<const uint32_t> drec = G(ps.drec);
   uint64_t b = drec[4 * r];
   uint32_t c = drec[4 * r + 1], po = drec[4 * r + 3];
-  u64x2 mine;
-  mine.x = 0;
-  mine.y = 0;
-  if (gl < c) mine = pool[po + gl];
-  uint64_t mine_in = (gl < c && has_in) ? G(a.in_scores)[mine.y] : 0;
+  gptr<const uint64_t> pw = G(reinterpret_cast<const uint64_t*>(ps.dpool));
+  uint64_t mine_k = 0;  // key and batch index of the bucket's key gl
+  uint32_t mine_i = 0;
+  if (gl < c) {
+    mine_k = pw[2 * (uint64_t)(po + gl)];
+    mine_i = (uint32_t)pw[2 * (uint64_t)(po + gl) + 1];
+  }
+  uint64_t mine_in = (gl < c && has_in) ? G(a.in_scores)[mine_i] : 0;
   while (true) {
     Bucket16 S;
     bucket_load(t, S, b, gl);
@@ -3786,20 +3830,22 @@ k_apply_deferred(TableView t, ApplyArgs a, PartScratch ps) {
       nc = drec[4 * rn + 1];
       npo = drec[4 * rn + 3];
     }
-    u64x2 nmine;
-    nmine.x = 0;
-    nmine.y = 0;
-    if (gl < nc) nmine = pool[npo + gl];
+    uint64_t nmine_k = 0;
+    uint32_t nmine_i = 0;
+    if (gl < nc) {
+      nmine_k = pw[2 * (uint64_t)(npo + gl)];
+      nmine_i = (uint32_t)pw[2 * (uint64_t)(npo + gl) + 1];
+    }
     uint64_t nin = 0;
-    if (kQueue) {
+    {
       DeferQ Q;
-      Q.ek0 = Q.ek1 = Q.ex0 = Q.ex1 = Q.ei0 = Q.ei1 = Q.ss0 = Q.ss1 = 0;
+      Q.ek = Q.ex = Q.ei = Q.ss0 = Q.ss1 = 0;
       uint32_t seg0 = 0;  // first key of the queue's segment
       for (uint32_t q = 0; q < c; q++) {  // uniform in the group
         uint64_t k, i, in;
         if (q < 16) {
-          k = shfl_u64(mine.x, (int)q, 16);
-          i = shfl_u64(mine.y, (int)q, 16);
+          k = shfl_u64(mine_k, (int)q, 16);
+          i = (uint32_t)__shfl((int)mine_i, (int)q, 16);
           in = shfl_u64(mine_in, (int)q, 16);
         } else {
           const u64x2 v = pool[po + q];
@@ -3814,24 +3860,8 @@ k_apply_deferred(TableView t, ApplyArgs a, PartScratch ps) {
         }
         defer_note(gl, Q, q - seg0, (uint32_t)i, act);
       }
-      nin = (gl < nc && has_in) ? G(a.in_scores)[nmine.y] : 0;
+      nin = (gl < nc && has_in) ? G(a.in_scores)[nmine_i] : 0;
       defer_run<OP, U>(t, a, b, gl, Q, c - seg0);
-    } else {
-      for (uint32_t q = 0; q < c; q++) {
-        uint64_t k, i, in;
-        if (q < 16) {
-          k = shfl_u64(mine.x, (int)q, 16);
-          i = shfl_u64(mine.y, (int)q, 16);
-          in = shfl_u64(mine_in, (int)q, 16);
-        } else {
-          const u64x2 v = pool[po + q];
-          k = v.x;
-          i = v.y;
-          in = has_in ? G(a.in_scores)[i] : 0;
-        }
-        apply_key_in<OP, U, true>(t, S, a, i, k, in);
-      }
-      nin = (gl < nc && has_in) ? G(a.in_scores)[nmine.y] : 0;
     }
     bucket_finish(t, S);
     if (rn >= nrec) break;
@@ -3839,7 +3869,8 @@ k_apply_deferred(TableView t, ApplyArgs a, PartScratch ps) {
     b = nb;
     c = nc;
     po = npo;
-    mine = nmine;
+    mine_k = nmine_k;
+    mine_i = nmine_i;
     mine_in = nin;
   }
 }
@@ -4573,13 +4604,13 @@ static void apply_part_op(const TableView& t, const ApplyArgs& a, const PartScra
   const dim3 gb(grid_for(a.n / kBigTile + kBigMax, 1, 1024));
 #define HKV_PART_U(UU)                                                                       \
   hipLaunchKernelGGL((k_apply_fast<OP, UU>), g, b, 0, s, t, a, ps);                          \
-  if (OP != OP_ASSIGN_SCORES && (OP != OP_INSERT_AND_EVICT || a.ev_bits) &&                  \
-      (OP != OP_ACCUM_OR_ASSIGN || UU >= acc_elem(a.value_type)))                            \
-    hipLaunchKernelGGL((k_apply_deferred<OP, UU, OP != OP_ASSIGN_SCORES>), gd, b, 0, s, t, a, ps); \
+  if ((OP == OP_INSERT_AND_EVICT && a.ev_bits) ||                                            \
+      (OP == OP_ACCUM_OR_ASSIGN && UU >= acc_elem(a.value_type)))                            \
+    hipLaunchKernelGGL((k_apply_deferred_q<OP == OP_ACCUM_OR_ASSIGN ? OP : OP_INSERT_AND_EVICT, UU>), \
+                       gd, b, 0, s, t, a, ps);                                               \
   else                                                                                       \
-    hipLaunchKernelGGL((k_apply_deferred<OP, UU, false>), gd, b, 0, s, t, a, ps);              \
+    hipLaunchKernelGGL((k_apply_deferred<OP, UU>), gd, b, 0, s, t, a, ps);                     \
   if (ps.big) {                                                                              \
-    hipLaunchKernelGGL(k_big_clear, dim3(kBigMax), b, 0, s, ps);                              \
     hipLaunchKernelGGL(k_big_count, gb, b, 0, s, t, ps);                                     \
     hipLaunchKernelGGL((k_big_fold<OP>), gb, b, 0, s, t, a, ps);                             \
   }                                                                                          \
