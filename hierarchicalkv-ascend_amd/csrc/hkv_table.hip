@@ -12,6 +12,7 @@
 #include <mutex>
 #include <new>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "../../include/hkv_amd.h"
@@ -227,19 +228,69 @@ struct hkv_table {
   // One slice of `nbk` buckets' rows: HBM while the budget lasts, then
   // pinned host memory (include/table.h:130-242).
   Slice alloc_slice(uint64_t nbk) {
-    const uint64_t bytes = std::max<uint64_t>(nbk * B * row, 256);
-    Slice s{nullptr, nullptr, true};
-    if (remaining_hbm >= bytes) {
-      hip_check(hipMalloc(&s.dev_ptr, bytes), "hipMalloc(values)");
-      remaining_hbm -= bytes;
-    } else {
-      hip_check(hipHostMalloc(&s.host_ptr, bytes, host_row_flags()), "hipHostMalloc(values)");
-      hip_check(hipHostGetDevicePointer((void**)&s.dev_ptr, s.host_ptr, 0),
-                "hipHostGetDevicePointer");
-      s.hbm = false;
-      pure_hbm = false;
+    std::vector<Slice> v = alloc_slices({nbk});
+    return v[0];
+  }
+
+  // Slices of nbk[j] buckets' rows, in order: HBM while the budget lasts,
+  // then pinned host memory.  The host slices are allocated by several host
+  // threads at once (pinning a fresh 2 GiB takes tens of milliseconds of one
+  // core); on any failure every slice of the call is released again.
+  std::vector<Slice> alloc_slices(const std::vector<uint64_t>& nbk) {
+    std::vector<Slice> out(nbk.size(), Slice{nullptr, nullptr, true});
+    std::vector<uint64_t> bytes(nbk.size());
+    std::vector<size_t> host;
+    uint64_t budget = remaining_hbm;
+    for (size_t j = 0; j < nbk.size(); j++) {
+      bytes[j] = std::max<uint64_t>(nbk[j] * B * row, 256);
+      if (budget >= bytes[j]) budget -= bytes[j];
+      else host.push_back(j);
     }
-    return s;
+    std::vector<hipError_t> err(nbk.size(), hipSuccess);
+    size_t hi = 0;
+    for (size_t j = 0; j < nbk.size(); j++) {
+      if (hi < host.size() && host[hi] == j) {
+        hi++;
+        continue;
+      }
+      err[j] = hipMalloc(&out[j].dev_ptr, bytes[j]);
+    }
+    const unsigned nth = (unsigned)std::min<size_t>(host.size(), 8);
+    auto pin = [&](unsigned w) {
+      if (hipSetDevice(device) != hipSuccess) {
+        for (size_t q = w; q < host.size(); q += nth) err[host[q]] = hipErrorInvalidDevice;
+        return;
+      }
+      for (size_t q = w; q < host.size(); q += nth) {
+        const size_t j = host[q];
+        Slice& sl = out[j];
+        sl.hbm = false;
+        err[j] = hipHostMalloc(&sl.host_ptr, bytes[j], host_row_flags());
+        if (err[j] == hipSuccess)
+          err[j] = hipHostGetDevicePointer((void**)&sl.dev_ptr, sl.host_ptr, 0);
+      }
+    };
+    if (nth <= 1) {
+      if (nth) pin(0);
+    } else {
+      std::vector<std::thread> th;
+      for (unsigned w = 0; w < nth; w++) th.emplace_back(pin, w);
+      for (auto& x : th) x.join();
+    }
+    for (size_t j = 0; j < nbk.size(); j++) {
+      if (err[j] == hipSuccess) continue;
+      for (auto& sl : out) {
+        if (sl.hbm && sl.dev_ptr) (void)hipFree(sl.dev_ptr);
+        if (!sl.hbm && sl.host_ptr) (void)hipHostFree(sl.host_ptr);
+      }
+      (void)hipGetLastError();
+      fail(HKV_ERR_DEVICE, std::string(out[j].hbm ? "hipMalloc(values): "
+                                                  : "hipHostMalloc(values): ") +
+                               hipGetErrorString(err[j]));
+    }
+    remaining_hbm = budget;
+    if (!host.empty()) pure_hbm = false;
+    return out;
   }
 
   // Allocates value rows for buckets [b0, b1).  Slice j holds buckets
@@ -269,7 +320,9 @@ struct hkv_table {
     } else if (slices.size() != (b0 >> slice_shift)) {
       fail(HKV_ERR_DEVICE, "value slices out of step with the bucket count");
     }
-    for (; b < b1; b += bps) slices.push_back(alloc_slice(std::min(bps, b1 - b)));
+    std::vector<uint64_t> nbk;
+    for (; b < b1; b += bps) nbk.push_back(std::min(bps, b1 - b));
+    for (const Slice& sl : alloc_slices(nbk)) slices.push_back(sl);
     if (slices.size() > d_slices_cap) {
       if (d_slices) hip_check(hipFree(d_slices), "hipFree");
       d_slices_cap = std::max<size_t>(slices.size() * 2, 16);
