@@ -1479,8 +1479,10 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
   gptr<u64x2> ent_w = G(reinterpret_cast<u64x2*>(ps.ent));  // in-place compaction
   gptr<uint64_t> trow = G(ps.trow);
   uint32_t added = 0;
-  // The partitions k_apply_fast left.
+  // The partitions k_apply_fast left (usually none: then every block leaves
+  // without touching the shared counter).
   const uint32_t nlist = *(volatile uint32_t*)&ps.dctr[2];
+  if (nlist == 0) return;
   // Blocks take partitions from a counter, so that a block holding a large
   // partition is not also given a fixed share of the others.
   for (;;) {
@@ -4595,7 +4597,10 @@ static void apply_part_op(const TableView& t, const ApplyArgs& a, const PartScra
   // with repeated keys list many partitions (every bucket with more than 32
   // keys lists its partition); two blocks of the multi-run kernel fit a CU
   // (LDS and registers), so for them 512 blocks take the list two per CU.
-  const dim3 gd(grid_for(a.n * 16, kBlock, 2048));
+  // The eviction kernels hold four waves per SIMD: 1024 blocks of 256
+  // threads fill 256 CUs in one round (a second round would double the cost
+  // of the usual empty launch).
+  const dim3 gd(grid_for(a.n * 16, kBlock, 1024));
   const uint32_t gpn = a.rule == RULE_TILE32 ? 512u : 256u;
   const dim3 gp(ps.np < gpn ? ps.np : gpn);
   const uint32_t nw = (uint32_t)((a.n + 31) / 32);
