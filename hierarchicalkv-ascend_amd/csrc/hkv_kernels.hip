@@ -2795,29 +2795,34 @@ __device__ __forceinline__ WinProbe probe_window(u32x4 w0, u32x4 w1, uint32_t st
 }
 
 // Probe of key k for the serial lane, over the bucket's digests in memory.
-// Slots filled by the call's earlier keys (bit set in f0..f3) show the empty
-// digest in memory; their keys are those of the entries [lo, e) (the earlier
-// keys of the bucket, in batch order) whose outcome took the slot.  Returns the slot holding k (*dup = 1), else the
-// first EMPTY slot when `empties` (*dup = 0), else -1.
+// Slots filled by the call's earlier keys (bit set in f0..f3) still show the
+// empty digest in memory and are skipped: the caller has already looked for
+// k among the keys those earlier keys placed (its scan of the bucket's
+// earlier entries), so only slots placed before the call can hold k here.
+// Returns the slot holding k (*dup = 1), else the first EMPTY slot when
+// `empties` (*dup = 0), else -1.  Digests load 32 slots (two 16-byte
+// chunks, in probe order) per memory round trip.
 __device__ __forceinline__ int probe_serial(const TableView& t, uint64_t base, uint32_t f0,
                                             uint32_t f1, uint32_t f2, uint32_t f3,
-                                            const uint64_t* s_key, const uint8_t* s_slot,
-                                            const uint8_t* s_fl, uint32_t lo, uint32_t e,
                                             uint32_t start, uint32_t d, uint64_t k, bool empties,
                                             int* dup) {
   const uint32_t B = t.B;
+  const uint32_t nch = B / 16;
   gptr<const u32x4> drow = (gptr<const u32x4>)(G(t.digests) + base);
   const uint32_t a = start & ~3u;
   const uint32_t rep = d * 0x01010101u;
   const uint32_t erep = (uint32_t)kEmptyDigest * 0x01010101u;
-  uint32_t cur = kNone;
-  u32x4 chunk = {0, 0, 0, 0};
+  uint32_t cur = kNone;  // chunk held in c0; c1 holds the next one
+  u32x4 c0 = {0, 0, 0, 0}, c1 = {0, 0, 0, 0};
   for (uint32_t off = 0; off < B + 4; off += 4) {
     const uint32_t g = (a + off) & (B - 1);
-    if ((g >> 4) != cur) {
-      cur = g >> 4;
-      chunk = drow[cur];
+    const uint32_t ch = g >> 4;
+    if (cur == kNone || (ch != cur && ch != ((cur + 1) & (nch - 1)))) {
+      cur = ch;
+      c0 = drow[ch];
+      c1 = drow[(ch + 1) & (nch - 1)];
     }
+    const u32x4 chunk = ch == cur ? c0 : c1;
     const uint32_t wi = (g >> 2) & 3;
     const uint32_t w = wi == 0 ? chunk.x : wi == 1 ? chunk.y : wi == 2 ? chunk.z : chunk.w;
     const uint32_t fm = (sel4(f0, f1, f2, f3, g >> 5) >> (g & 31)) & 0xFu;
@@ -2829,16 +2834,6 @@ __device__ __forceinline__ int probe_serial(const TableView& t, uint64_t base, u
         *dup = 1;
         return (int)(g + j);
       }
-    }
-    uint32_t fq = fm;
-    while (fq) {
-      const uint32_t p = g + __builtin_ctz(fq);
-      fq &= fq - 1;
-      for (uint32_t x = lo; x < e; x++)
-        if (s_slot[x] == p && (s_fl[x] & kResMask) == kResNew && s_key[x] == k) {
-          *dup = 1;
-          return (int)p;
-        }
     }
     if (!empties) continue;
     uint32_t em = eq_bytes4(w, erep) & ~fm;
@@ -3388,7 +3383,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
         }
       }
       if (!known)
-        sl = probe_serial(t, base, f0, f1, f2, f3, s_key, s_slot, s_fl, lo, e, start, d, k,
+        sl = probe_serial(t, base, f0, f1, f2, f3, start, d, k,
                           !may_insert || bsz < B, &dup);
       if (sl < 0 && may_insert) {
         // The eviction path: the rest of the bucket goes to k_apply_deferred.
