@@ -79,11 +79,13 @@ struct PartScratch {
   uint32_t* pinfo;      // [partitions][2]: first entry, entry count
   uint32_t* spill_top;  // entries placed past the fixed regions
   uint64_t* trow;       // [n] row task per batch index, zero between calls
-  uint32_t* plist;      // [partitions] partitions the single-run kernel left
+  uint32_t* plist;      // [partitions] partitions the single-run kernel left: whole ones
+                        // from the front, long-bucket-only ones from the back
   uint32_t* drec;       // [n][4] buckets handed to the 16-lane kernel
   uint64_t* dpool;      // [n][2] their keys, {key, batch index}
-  uint32_t* dctr;       // [8] records, pool entries, listed partitions, partitions taken,
-                        // big partitions listed (zeroed by the count kernel)
+  uint32_t* dctr;       // [8] records, pool entries, whole partitions listed, partitions
+                        // taken, big partitions listed, long-bucket-only partitions
+                        // listed (zeroed by the count kernel)
   uint32_t* ev_bits;    // [n / 32 + 1] insert_and_evict record flags, zero between calls
   uint32_t* ev_wpre;    // [n / 32 + 1] set bits before each word, within its block of 256 words
   uint32_t* ev_blk;     // [n / 8192 + 3] block offsets, then the record count and records below it

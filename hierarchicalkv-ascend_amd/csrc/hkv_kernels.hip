@@ -1058,6 +1058,7 @@ __global__ __launch_bounds__(kBlock) void k_pcount(TableView t, const uint64_t* 
     ps.dctr[2] = 0;
     ps.dctr[3] = 0;
     ps.dctr[4] = 0;
+    ps.dctr[5] = 0;
   }
   uint32_t* H = ps.hist + (uint64_t)blockIdx.x * NP;
   for (uint32_t p0 = 0; p0 < NP; p0 += ps.prange) {
@@ -1480,17 +1481,21 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
   gptr<uint64_t> trow = G(ps.trow);
   uint32_t added = 0;
   // The partitions k_apply_fast left (usually none: then every block leaves
-  // without touching the shared counter).
-  const uint32_t nlist = *(volatile uint32_t*)&ps.dctr[2];
+  // without touching the shared counter): whole partitions from the front of
+  // the list, long-bucket-only ones from its back.
+  const uint32_t nwhole = *(volatile uint32_t*)&ps.dctr[2];
+  const uint32_t nlist = nwhole + *(volatile uint32_t*)&ps.dctr[5];
   if (nlist == 0) return;
   // Blocks take partitions from a counter, so that a block holding a large
-  // partition is not also given a fixed share of the others.
+  // partition is not also given a fixed share of the others.  The whole
+  // partitions, which take a block two to three times as long, go first:
+  // taken last, one of them would set the kernel's end.
   for (;;) {
     if (tid == 0) s_li = atomicAdd(&ps.dctr[3], 1u);
     __syncthreads();
     const uint32_t li = s_li;
     if (li >= nlist) break;  // block-uniform
-    const uint32_t pl = ps.plist[li];
+    const uint32_t pl = li < nwhole ? ps.plist[li] : ps.plist[ps.np - 1 - (li - nwhole)];
     // kPartLongOnly: k_apply_fast applied the buckets with at most kLaneMax
     // entries; only the longer ones are folded (or walked) here.
     const bool long_only = (pl & kPartLongOnly) != 0;
@@ -3100,7 +3105,8 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
       if (tid == 0) ps.plist[atomicAdd(&ps.dctr[2], 1u)] = p;
       return;
     }
-    if (s_big == 2 && tid == 0) ps.plist[atomicAdd(&ps.dctr[2], 1u)] = p | kPartLongOnly;
+    if (s_big == 2 && tid == 0)
+      ps.plist[ps.np - 1 - atomicAdd(&ps.dctr[5], 1u)] = p | kPartLongOnly;
 #pragma unroll
     for (uint32_t q = 0; q < kPer; q++) {
       if (tid + q * kBlock < m_all && !s_long[lb[q]]) {
