@@ -2722,6 +2722,7 @@ constexpr uint8_t kResNew = 1 << 4;   // absent; the slot is the probe's first E
 constexpr uint8_t kResDup = 2 << 4;   // present at the slot
 constexpr uint8_t kResSlow = 3 << 4;  // undecided by the window (or needs the serial lane)
 constexpr uint8_t kResMask = 3 << 4;
+constexpr uint8_t kRepeat = 1 << 6;  // a later occurrence of a key met earlier in its bucket
 
 __device__ __forceinline__ uint32_t sel4(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3,
                                          uint32_t q) {
@@ -3041,6 +3042,14 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
   const bool has_in = a.in_scores != nullptr;
   const bool old_for_hit = a.sc.strategy == kLfu || a.sc.strategy == kEpochLfu;
   const bool old_for_new = a.sc.strategy == kLfu && !has_in;
+  // Batches with repeated keys: a key's later occurrences in its bucket are
+  // applied beside its first one (step F), with the scores folded as the
+  // sequential updates would leave them.  The fold needs the input scores of
+  // the strategies that add them up (and of kCustomized, whose last one wins).
+  const bool fold = (OP == OP_FIND_OR_INSERT || OP == OP_INSERT_OR_ASSIGN) &&
+                    a.rule == RULE_TILE32 &&
+                    (has_in || !(a.sc.strategy == kLfu || a.sc.strategy == kEpochLfu ||
+                                 a.sc.strategy == kCustomized));
 
   /* A. Entries grouped by bucket (every load issued before the first use;
         indices past m_all read entry m_all - 1 and are ignored).  A bucket
@@ -3196,6 +3205,20 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
       if (e >= m) continue;
       const uint64_t k = s_key[e];
       const uint64_t in = s_sc[e];
+      if (fold) {
+        // A repeat takes the outcome of the key's first occurrence (step F);
+        // its input score stays in s_sc for the fold.
+        const uint32_t lo = s_off[(uint32_t)((gi[q] >> t.bshift) % kPartBuckets)];
+        bool rep = false;
+        for (uint32_t x = lo; x < e; x++) rep |= s_key[x] == k;
+        if (rep) {
+          s_slot[e] = kNoSlot;
+#pragma unroll
+          for (uint32_t j = 0; j < kMoreEmpty; j++) s_more[j][e] = kNoSlot;
+          s_fl[e] = kResSlow | kRepeat;
+          continue;
+        }
+      }
       uint8_t fl = kResSlow, slot = kNoSlot;
       uint64_t sc = 0;
       // A verified digest match is the first one in probe order, so the key
@@ -3249,9 +3272,11 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
     const uint32_t lo = s_off[lbk];
     const uint32_t r = e - lo;
     const uint32_t res = s_fl[e] & kResMask;
+    if (s_fl[e] & kRepeat) continue;  // follows the key's first occurrence
     bool bad = res == kResSlow;
     uint32_t nnew = 0;
     for (uint32_t x = lo; x < e; x++) {
+      if (s_fl[x] & kRepeat) continue;  // a repeat takes no slot
       if (s_key[x] == k) bad = true;
       if ((s_fl[x] & kResMask) == kResNew) {
         nnew++;
@@ -3262,6 +3287,47 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
     if (bad) atomicMin(&s_cnt[lbk], r);
   }
   lds_barrier();
+
+  /* F. Repeats below a bucket's stop rank: hits at the slot of the key's
+        first occurrence, whose record carries the score the sequential
+        updates leave (the first occurrence's score, then the fold of the
+        repeats' inputs).  find_or_insert reads the row the first occurrence
+        wrote (a new key) or the table row; insert_or_assign keeps the last
+        occurrence's row write only. */
+  if (fold) {
+#pragma unroll
+    for (uint32_t q = 0; q < kPer; q++) {
+      const uint32_t e = tid + q * kBlock;
+      if (e >= m) continue;
+      const uint8_t f = s_fl[e];
+      const uint32_t res = f & kResMask;
+      if ((f & kRepeat) || (res != kResDup && res != kResNew)) continue;
+      const uint64_t k = s_key[e];
+      const uint32_t lbk = (uint32_t)(bucket_of(t, k) % kPartBuckets);
+      const uint32_t lo = s_off[lbk], c = s_off[lbk + 1] - lo;
+      const uint32_t end = lo + (s_cnt[lbk] < c ? s_cnt[lbk] : c);
+      if (e >= end) continue;
+      uint64_t sum = 0, in_last = 0;
+      uint32_t last = kNone;
+      for (uint32_t x = e + 1; x < end; x++) {
+        if (s_key[x] != k) continue;
+        const uint64_t in = s_sc[x];
+        sum += a.sc.strategy == kLfu ? in : (in & kScoreMask);
+        in_last = in;
+        last = x;
+      }
+      if (last == kNone) continue;
+      s_sc[e] = heavy_score<OP>(a.sc, has_in, false, s_sc[e], sum, in_last);
+      const uint8_t tk = OP == OP_FIND_OR_INSERT ? (res == kResNew ? kTkFwd : kTkOut) : kTkIn;
+      for (uint32_t x = e + 1; x < end; x++) {
+        if (s_key[x] != k) continue;
+        s_slot[x] = s_slot[e];
+        s_fl[x] = kResDup | kRepeat | ((OP == OP_INSERT_OR_ASSIGN && x != last) ? 0 : tk);
+      }
+      if (OP == OP_INSERT_OR_ASSIGN) s_fl[e] = f & (uint8_t)~kTkMask;  // superseded
+    }
+    lds_barrier();
+  }
 
   /* S. The rest of a bucket whose parallel pass stopped, by one lane.  Such
         buckets are listed so that consecutive lanes take them: the serial

@@ -77,6 +77,41 @@ def test_single_run_repeated_keys(strategy):
     p.assert_same_state()
 
 
+@pytest.mark.parametrize("op", ["insert_or_assign", "find_or_insert"])
+@pytest.mark.parametrize("strategy,scores,ignore", [
+    (O.LRU, False, False), (O.LRU, True, True), (O.LFU, True, False),
+    (O.EPOCH_LFU, True, False), (O.EPOCH_LFU, True, True), (O.EPOCH_LRU, False, False),
+    (O.CUSTOMIZED, True, False)])
+def test_single_run_repeat_fold(op, strategy, scores, ignore):
+    """unique_key=false batches on the single-run route where keys repeat a
+    few times inside a bucket: later occurrences are hits at the first one's
+    slot, with the scores the sequential updates leave (EpochLfu inputs near
+    2^31 saturate the low word).  The table fills to a load factor near 1.0,
+    so repeats also fall past a bucket's first serial or evicting key."""
+    rng = np.random.default_rng(305 + strategy)
+    cap = 1 << 16
+    p = Pair(cap, dim=4, strategy=strategy)
+    p.set_global_epoch(5)
+    hot = uniform_keys(rng, 300)
+    pool = uniform_keys(rng, 72000, exclude=hot)
+    for b in range(90):
+        ks = np.concatenate([rng.choice(hot, 256), pool[b * 800 + rng.permutation(800)[:768]]])
+        ks = ks[rng.permutation(ks.size)]
+        sc = None
+        if scores:
+            hi = (1 << 31) if strategy == O.EPOCH_LFU else (1 << 20)
+            sc = rng.integers(1, hi, ks.size, dtype=np.uint64)
+        v = rand_vals(rng, ks.size, 4)
+        if op == "insert_or_assign":
+            p.insert_or_assign(ks, v, sc, unique_key=False, ignore=ignore, clock=11 + b)
+        else:
+            ov, gv = p.find_or_insert(ks, v, sc, unique_key=False, ignore=ignore, clock=11 + b)
+            np.testing.assert_array_equal(gv.view(np.uint8), ov.view(np.uint8))
+        if b % 30 == 29:
+            p.assert_same_state()
+    assert p.g.load_factor() > 0.95
+
+
 @pytest.mark.parametrize("unique", [True, False])
 def test_single_run_find_or_insert_reads_same_batch_rows(unique):
     """find_or_insert with keys repeated in a batch: the later occurrences
