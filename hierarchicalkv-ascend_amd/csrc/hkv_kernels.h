@@ -114,15 +114,8 @@ void launch_find_missed(const TableView& t, const uint64_t* keys, uint64_t n,
                         uint64_t* scores, int unit, hipStream_t s);
 void launch_erase(const TableView& t, const uint64_t* keys, uint64_t n,
                   hipStream_t s);
-// A second stream and two events owned by the table: the eviction kernel
-// (k_apply_deferred*) is forked onto `s` after the single-run kernel and
-// joined back before the call's last kernels.  A null stream runs it in line.
-struct SideStream {
-  hipStream_t s;
-  hipEvent_t fork, join;
-};
 void launch_apply_part(const TableView& t, int op, const ApplyArgs& a,
-                       const PartScratch& ps, hipStream_t s, const SideStream& side);
+                       const PartScratch& ps, hipStream_t s);
 // Pointer find_or_insert: placement in batch order, slot words in
 // ps.trow, then value / key addresses, founds, and (unless keep_locked) the
 // keys written back over LOCKED.

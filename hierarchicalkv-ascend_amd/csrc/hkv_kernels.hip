@@ -4653,7 +4653,7 @@ void launch_erase(const TableView& t, const uint64_t* keys, uint64_t n, hipStrea
 
 template <int OP>
 static void apply_part_op(const TableView& t, const ApplyArgs& a, const PartScratch& ps,
-                          hipStream_t s, const SideStream& side) {
+                          hipStream_t s) {
   const size_t lds = (size_t)(ps.np < ps.prange ? ps.np : ps.prange) * sizeof(uint32_t);
   hipLaunchKernelGGL(k_pcount, dim3(ps.chunks), dim3(kBlock), lds, s, t, a.keys, a.n, ps);
   hipLaunchKernelGGL(k_pscan, dim3((ps.np + 15) / 16), dim3(1024), 0, s, ps);
@@ -4674,28 +4674,14 @@ static void apply_part_op(const TableView& t, const ApplyArgs& a, const PartScra
   const uint32_t nbw = (nw + kEvBlkWords - 1) / kEvBlkWords;
   // Big partitions: at most n / kBigPart of them, kBigTile entries per tile.
   const dim3 gb(grid_for(a.n / kBigTile + kBigMax, 1, 1024));
-  // The eviction kernel and the multi-run kernel own disjoint buckets (the
-  // single-run kernel hands each bucket to at most one of them), so the
-  // eviction kernel runs on the table's second stream beside the
-  // multi-run and big-partition kernels, and is joined back before the
-  // record compaction and the end of the call.
-  bool fork = false;
-  hipStream_t sd = s;
 #define HKV_PART_U(UU)                                                                       \
   hipLaunchKernelGGL((k_apply_fast<OP, UU>), g, b, 0, s, t, a, ps);                          \
-  fork = side.s && hipEventRecord(side.fork, s) == hipSuccess &&                             \
-         hipStreamWaitEvent(side.s, side.fork, 0) == hipSuccess;                             \
-  sd = fork ? side.s : s;                                                                    \
   if ((OP == OP_INSERT_AND_EVICT && a.ev_bits) ||                                            \
       (OP == OP_ACCUM_OR_ASSIGN && UU >= acc_elem(a.value_type)))                            \
     hipLaunchKernelGGL((k_apply_deferred_q<OP == OP_ACCUM_OR_ASSIGN ? OP : OP_INSERT_AND_EVICT, UU>), \
-                       gd, b, 0, sd, t, a, ps);                                              \
+                       gd, b, 0, s, t, a, ps);                                               \
   else                                                                                       \
-    hipLaunchKernelGGL((k_apply_deferred<OP, UU>), gd, b, 0, sd, t, a, ps);                    \
-  if (fork && hipEventRecord(side.join, sd) != hipSuccess) {                                 \
-    (void)hipStreamSynchronize(sd);                                                          \
-    fork = false;                                                                            \
-  }                                                                                          \
+    hipLaunchKernelGGL((k_apply_deferred<OP, UU>), gd, b, 0, s, t, a, ps);                     \
   if (ps.big) {                                                                              \
     hipLaunchKernelGGL(k_big_count, gb, b, 0, s, t, ps);                                     \
     hipLaunchKernelGGL((k_big_fold<OP>), gb, b, 0, s, t, a, ps);                             \
@@ -4705,8 +4691,6 @@ static void apply_part_op(const TableView& t, const ApplyArgs& a, const PartScra
     hipLaunchKernelGGL((k_big_tasks<OP, UU>), gb, b, 0, s, t, a, ps);                        \
   if (OP == OP_FIND_OR_INSERT)                                                               \
     hipLaunchKernelGGL((k_rowtasks<UU>), dim3(grid_for(a.n, kBlock, 2048)), b, 0, s, t, a, ps); \
-  if (fork && hipStreamWaitEvent(s, side.join, 0) != hipSuccess)                             \
-    (void)hipStreamSynchronize(sd);                                                          \
   if (OP == OP_INSERT_AND_EVICT && a.ev_bits) {                                              \
     hipLaunchKernelGGL(k_evc_count, dim3(nbw), b, 0, s, ps.ev_bits, nw, ps.ev_wpre, ps.ev_blk); \
     hipLaunchKernelGGL(k_evc_scan, dim3(1), b, 0, s, ps.ev_blk, nbw, ps.ev_bits, ps.ev_wpre,   \
@@ -4727,13 +4711,13 @@ static void apply_part_op(const TableView& t, const ApplyArgs& a, const PartScra
 }
 
 void launch_apply_part(const TableView& t, int op, const ApplyArgs& a, const PartScratch& ps,
-                       hipStream_t s, const SideStream& side) {
+                       hipStream_t s) {
   switch (op) {
-    case OP_INSERT_OR_ASSIGN: apply_part_op<OP_INSERT_OR_ASSIGN>(t, a, ps, s, side); break;
-    case OP_FIND_OR_INSERT: apply_part_op<OP_FIND_OR_INSERT>(t, a, ps, s, side); break;
-    case OP_INSERT_AND_EVICT: apply_part_op<OP_INSERT_AND_EVICT>(t, a, ps, s, side); break;
-    case OP_ACCUM_OR_ASSIGN: apply_part_op<OP_ACCUM_OR_ASSIGN>(t, a, ps, s, side); break;
-    default: apply_part_op<OP_ASSIGN_SCORES>(t, a, ps, s, side); break;
+    case OP_INSERT_OR_ASSIGN: apply_part_op<OP_INSERT_OR_ASSIGN>(t, a, ps, s); break;
+    case OP_FIND_OR_INSERT: apply_part_op<OP_FIND_OR_INSERT>(t, a, ps, s); break;
+    case OP_INSERT_AND_EVICT: apply_part_op<OP_INSERT_AND_EVICT>(t, a, ps, s); break;
+    case OP_ACCUM_OR_ASSIGN: apply_part_op<OP_ACCUM_OR_ASSIGN>(t, a, ps, s); break;
+    default: apply_part_op<OP_ASSIGN_SCORES>(t, a, ps, s); break;
   }
 }
 

@@ -192,12 +192,6 @@ struct hkv_table {
   uint64_t blk_cap = 0;
   // size scratch
   uint64_t* d_sum = nullptr;
-  // Second stream of the insert-like calls with repeated keys: the eviction
-  // kernel runs there beside the multi-run kernel (they own disjoint
-  // buckets), forked from and joined back into the caller's stream with the
-  // two events.
-  hipStream_t side = nullptr;
-  hipEvent_t ev_fork = nullptr, ev_join = nullptr;
   uint64_t* h_sum = nullptr;
 
   TableView view() const {
@@ -367,9 +361,6 @@ struct hkv_table {
     (void)hipFree(p_big);
     (void)hipFree(p_bigpart);
     (void)hipFree(blk);
-    if (side) (void)hipStreamDestroy(side);
-    if (ev_fork) (void)hipEventDestroy(ev_fork);
-    if (ev_join) (void)hipEventDestroy(ev_join);
     (void)hipFree(d_sum);
     if (h_sum) (void)hipHostFree(h_sum);
   }
@@ -763,12 +754,7 @@ int insert_like(hkv_table* t, int op, uint64_t n, const void* keys, const void* 
     if (rule == RULE_TILE32 && op != OP_ACCUM_OR_ASSIGN) t->big_scratch(&ps);
   }
   if (op == OP_INSERT_AND_EVICT) a.ev_bits = ps.ev_bits;
-  // The fork and join cost the caller's stream about 15 us, which pays only
-  // where the multi-run kernel has work beside the eviction kernel: batches
-  // with repeated keys (the big-partition path is on for them).
-  const SideStream side = ps.big ? SideStream{t->side, t->ev_fork, t->ev_join}
-                                 : SideStream{nullptr, nullptr, nullptr};
-  launch_apply_part(t->view(), op, a, ps, s, side);
+  launch_apply_part(t->view(), op, a, ps, s);
   hip_check(hipGetLastError(), "kernel launch");
   return HKV_OK;
 }
@@ -877,9 +863,6 @@ int hkv_create(const hkv_options* o, int key_type, int value_type, int strategy,
       hip_check(hipHostMalloc(&t->h_sum, sizeof(uint64_t), hipHostMallocDefault),
                 "hipHostMalloc(sum)");
       resolve_noalloc_scratch(t->device);
-      hip_check(hipStreamCreateWithFlags(&t->side, hipStreamNonBlocking), "hipStreamCreate");
-      hip_check(hipEventCreateWithFlags(&t->ev_fork, hipEventDisableTiming), "hipEventCreate");
-      hip_check(hipEventCreateWithFlags(&t->ev_join, hipEventDisableTiming), "hipEventCreate");
       t->add_slices(0, t->nb, 0);
       launch_init_slots(t->view(), 0, t->nb, 0);
       launch_fill_u64(t->live, 0, 1, 0);
