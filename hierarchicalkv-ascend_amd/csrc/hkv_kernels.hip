@@ -1074,17 +1074,18 @@ __global__ __launch_bounds__(kBlock) void k_pcount(TableView t, const uint64_t* 
   }
 }
 
-// 16 partitions per block of 1024 threads; thread (segment group sg, column
-// c) handles chunks [sg * per, (sg + 1) * per) of partition c, so that each
-// block row of 16 columns reads 64 contiguous bytes per chunk.
-constexpr uint32_t kScanGroups = 64;
+// kScanCols partitions per block of 1024 threads; thread (segment group sg,
+// column c) handles chunks [sg * per, (sg + 1) * per) of partition c, so that
+// each block row reads 128 contiguous bytes (one whole cache line) per chunk.
+constexpr uint32_t kScanCols = 32;
+constexpr uint32_t kScanGroups = 1024 / kScanCols;
 
 __global__ __launch_bounds__(1024) void k_pscan(PartScratch ps) {
-  constexpr uint32_t kReg = 16;  // column values a thread keeps in registers
-  __shared__ uint32_t s_part[kScanGroups][16];
-  __shared__ uint32_t s_base[16];
-  const uint32_t c = threadIdx.x & 15, sg = threadIdx.x >> 4;
-  const uint32_t p = blockIdx.x * 16 + c;
+  constexpr uint32_t kReg = 32;  // column values a thread keeps in registers
+  __shared__ uint32_t s_part[kScanGroups][kScanCols];
+  __shared__ uint32_t s_base[kScanCols];
+  const uint32_t c = threadIdx.x % kScanCols, sg = threadIdx.x / kScanCols;
+  const uint32_t p = blockIdx.x * kScanCols + c;
   const uint32_t NP = ps.np, NG = ps.chunks;
   const uint32_t per = (NG + kScanGroups - 1) / kScanGroups;
   const uint32_t g0 = sg * per < NG ? sg * per : NG;
@@ -4656,7 +4657,7 @@ static void apply_part_op(const TableView& t, const ApplyArgs& a, const PartScra
                           hipStream_t s) {
   const size_t lds = (size_t)(ps.np < ps.prange ? ps.np : ps.prange) * sizeof(uint32_t);
   hipLaunchKernelGGL(k_pcount, dim3(ps.chunks), dim3(kBlock), lds, s, t, a.keys, a.n, ps);
-  hipLaunchKernelGGL(k_pscan, dim3((ps.np + 15) / 16), dim3(1024), 0, s, ps);
+  hipLaunchKernelGGL(k_pscan, dim3((ps.np + kScanCols - 1) / kScanCols), dim3(1024), 0, s, ps);
   hipLaunchKernelGGL(k_pscatter, dim3(ps.chunks), dim3(kBlock), lds, s, t, a.keys, a.n, ps);
   const dim3 g(ps.np), b(kBlock);
   // After the single-run kernel, the eviction path and the multi-run kernel
@@ -4728,7 +4729,7 @@ void launch_find_or_insert_ptr(const TableView& t, const ApplyArgs& a0, const Pa
   a.slot_out = ps.trow;
   const size_t lds = (size_t)(ps.np < ps.prange ? ps.np : ps.prange) * sizeof(uint32_t);
   hipLaunchKernelGGL(k_pcount, dim3(ps.chunks), dim3(kBlock), lds, s, t, a.keys, a.n, ps);
-  hipLaunchKernelGGL(k_pscan, dim3((ps.np + 15) / 16), dim3(1024), 0, s, ps);
+  hipLaunchKernelGGL(k_pscan, dim3((ps.np + kScanCols - 1) / kScanCols), dim3(1024), 0, s, ps);
   hipLaunchKernelGGL(k_pscatter, dim3(ps.chunks), dim3(kBlock), lds, s, t, a.keys, a.n, ps);
   const dim3 gp(ps.np < 2048 ? ps.np : 2048), b(kBlock);
   hipLaunchKernelGGL((k_apply_seq<OP_FIND_OR_INSERT_PTR, 16>), gp, b, 0, s, t, a, ps);

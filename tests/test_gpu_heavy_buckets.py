@@ -250,3 +250,34 @@ def test_long_buckets_accum():
         p.accum_or_assign(q, rng.uniform(-0.01, 0.01, (q.size, dim)).astype(np.float32), flags,
                           scores_for(strategy, rng, q.size), clock=11)
         p.assert_same_state()
+
+
+@pytest.mark.parametrize("op", ["find_or_insert", "insert_or_assign", "insert_and_evict",
+                                "assign_scores"])
+@pytest.mark.parametrize("strategy", STRATS)
+def test_partitions_beyond_one_load(op, strategy):
+    """Partitions of 705-4096 entries (hot keys repeated hundreds of times)
+    go to the multi-run kernel whole: its fold takes the hot buckets and its
+    run loop the short ones, including a partition with more short-bucket
+    entries than one LDS run holds (36 buckets of 22 keys of their own, in
+    partition 3)."""
+    rng = np.random.default_rng(420 + strategy)
+    cap, dim = 1 << 17, 4
+    p = Pair(cap, dim=dim, strategy=strategy)
+    p.set_global_epoch(6)
+    base = uniform_keys(rng, 40000)
+    p.insert_or_assign(base, rand_vals(rng, base.size, dim),
+                       scores_for(strategy, rng, base.size), clock=10)
+    p.assert_same_state()
+    crowd = np.concatenate([keys_in_bucket(rng, 22, cap, 768 + 7 * j, lo=1 << 40, hi=1 << 62)
+                            for j in range(36)])
+    for r in range(3):
+        p.set_global_epoch(7 + r)
+        fresh = uniform_keys(rng, 602, exclude=np.concatenate([base, crowd]))
+        hot = np.concatenate([rng.choice(base, 2, replace=False), fresh[:2]])
+        q = np.concatenate([np.repeat(hot[0], 1500), np.repeat(hot[1], 60),
+                            np.repeat(hot[2], 900), np.repeat(hot[3], 40),
+                            rng.choice(base, 900), rng.choice(fresh[2:], 900), crowd])
+        q = q[rng.permutation(q.size)]
+        _run(p, op if r else "find_or_insert", rng, q, strategy, dim, clock=50 + r,
+             big=(r == 2))
