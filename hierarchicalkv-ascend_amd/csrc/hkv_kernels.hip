@@ -1040,6 +1040,18 @@ __device__ __forceinline__ void chunk_parts(const TableView& t, const uint64_t* 
     pq[q] = is_reserved(kq[q]) ? kNone : (uint32_t)(bucket_of(t, kq[q]) / kPartBuckets);
 }
 
+// Chunk of block b of nb: workgroups are dispatched round-robin over the
+// chip's 8 XCDs, so this gives the blocks of one XCD a contiguous range of
+// chunks.  A partition's segments from neighbouring chunks are adjacent in
+// the entry array, so its cache lines are then written through one XCD's L2
+// (and the scatter finds the chunk's keys in the L2 the count read them
+// through).
+__device__ __forceinline__ uint32_t xcd_chunk(uint32_t b, uint32_t nb) {
+  constexpr uint32_t kXcds = 8;
+  const uint32_t full = nb / kXcds * kXcds;
+  return b < full ? (b % kXcds) * (nb / kXcds) + b / kXcds : b;
+}
+
 // The LDS histogram holds ps.prange partitions; a table with more partitions
 // is counted in several passes over the chunk's keys, which stay in registers.
 __global__ __launch_bounds__(kBlock) void k_pcount(TableView t, const uint64_t* __restrict__ keys,
@@ -1047,7 +1059,8 @@ __global__ __launch_bounds__(kBlock) void k_pcount(TableView t, const uint64_t* 
   extern __shared__ uint32_t s_h[];
   constexpr uint32_t kPer = kPartChunk / kBlock;
   const uint32_t NP = ps.np;
-  const uint64_t i0 = (uint64_t)blockIdx.x * kPartChunk;
+  const uint32_t g = xcd_chunk(blockIdx.x, gridDim.x);
+  const uint64_t i0 = (uint64_t)g * kPartChunk;
   uint64_t kq[kPer];
   uint32_t pq[kPer];
   chunk_parts(t, keys, n, i0, kq, pq);
@@ -1060,7 +1073,7 @@ __global__ __launch_bounds__(kBlock) void k_pcount(TableView t, const uint64_t* 
     ps.dctr[4] = 0;
     ps.dctr[5] = 0;
   }
-  uint32_t* H = ps.hist + (uint64_t)blockIdx.x * NP;
+  uint32_t* H = ps.hist + (uint64_t)g * NP;
   for (uint32_t p0 = 0; p0 < NP; p0 += ps.prange) {
     const uint32_t w = NP - p0 < ps.prange ? NP - p0 : ps.prange;
     for (uint32_t q = threadIdx.x; q < w; q += kBlock) s_h[q] = 0;
@@ -1143,11 +1156,12 @@ __global__ __launch_bounds__(kBlock) void k_pscatter(TableView t,
   extern __shared__ uint32_t s_o[];
   constexpr uint32_t kPer = kPartChunk / kBlock;
   const uint32_t NP = ps.np;
-  const uint64_t i0 = (uint64_t)blockIdx.x * kPartChunk;
+  const uint32_t g = xcd_chunk(blockIdx.x, gridDim.x);
+  const uint64_t i0 = (uint64_t)g * kPartChunk;
   uint64_t kq[kPer];
   uint32_t pq[kPer];
   chunk_parts(t, keys, n, i0, kq, pq);
-  const uint32_t* H = ps.hist + (uint64_t)blockIdx.x * NP;
+  const uint32_t* H = ps.hist + (uint64_t)g * NP;
   gptr<u64x2> ent = G(reinterpret_cast<u64x2*>(ps.ent));
   for (uint32_t p0 = 0; p0 < NP; p0 += ps.prange) {
     const uint32_t w = NP - p0 < ps.prange ? NP - p0 : ps.prange;
