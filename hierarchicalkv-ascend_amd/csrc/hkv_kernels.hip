@@ -3276,30 +3276,55 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
   }
   lds_barrier();
 
-  /* C. Per bucket, the first key whose parallel outcome may differ from the
-        sequential one. */
+  /* C. Per bucket, by its thread in batch order, the first key whose
+        outcome the parallel pass cannot decide: an undecided probe, a key
+        met again (without the fold of step F), a new key that would find the
+        bucket full, or a new key whose recorded EMPTY slots earlier new keys
+        of the call all took.  A new key whose first EMPTY slot an earlier
+        one took moves to the next EMPTY slot of its window: its probe passes
+        the taken slot, and no key is present past an EMPTY slot. */
+  {
+    const uint32_t bk = tid;
+    const uint32_t lo = s_off[bk], hi = s_off[bk + 1];
+    uint32_t tk0 = 0, tk1 = 0, tk2 = 0, tk3 = 0;  // slots taken by the call's new keys
+    uint32_t nnew = 0, stop = kNone;
+    for (uint32_t e = lo; e < hi; e++) {
+      const uint8_t f = s_fl[e];
+      if (f & kRepeat) continue;  // follows the key's first occurrence
+      const uint32_t res = f & kResMask;
+      bool bad = res == kResSlow;
+      if (!bad && !fold) {
+        const uint64_t k = s_key[e];
+        for (uint32_t x = lo; x < e; x++) bad |= s_key[x] == k;
+      }
+      if (!bad && res == kResNew) {
+        bad = s_bsz[bk] + nnew >= B;
+        uint32_t sl = s_slot[e];
 #pragma unroll
-  for (uint32_t q = 0; q < kPer; q++) {
-    const uint32_t e = tid + q * kBlock;
-    if (e >= m) continue;
-    const uint64_t k = s_key[e];
-    const uint32_t lbk = (uint32_t)(bucket_of(t, k) % kPartBuckets);
-    const uint32_t lo = s_off[lbk];
-    const uint32_t r = e - lo;
-    const uint32_t res = s_fl[e] & kResMask;
-    if (s_fl[e] & kRepeat) continue;  // follows the key's first occurrence
-    bool bad = res == kResSlow;
-    uint32_t nnew = 0;
-    for (uint32_t x = lo; x < e; x++) {
-      if (s_fl[x] & kRepeat) continue;  // a repeat takes no slot
-      if (s_key[x] == k) bad = true;
-      if ((s_fl[x] & kResMask) == kResNew) {
-        nnew++;
-        if (res == kResNew && s_slot[x] == s_slot[e]) bad = true;
+        for (uint32_t j = 0; j <= kMoreEmpty; j++) {
+          if (bad || sl == kNoSlot) break;
+          const uint32_t w = sl >> 5, bit = 1u << (sl & 31);
+          const uint32_t cur = w == 0 ? tk0 : w == 1 ? tk1 : w == 2 ? tk2 : tk3;
+          if (!(cur & bit)) break;  // free: the key takes it
+          sl = j < kMoreEmpty ? s_more[j][e] : kNoSlot;
+        }
+        if (sl == kNoSlot) bad = true;
+        if (!bad) {
+          s_slot[e] = (uint8_t)sl;
+          const uint32_t w = sl >> 5, bit = 1u << (sl & 31);
+          tk0 |= w == 0 ? bit : 0u;
+          tk1 |= w == 1 ? bit : 0u;
+          tk2 |= w == 2 ? bit : 0u;
+          tk3 |= w == 3 ? bit : 0u;
+          nnew++;
+        }
+      }
+      if (bad) {
+        stop = e - lo;
+        break;
       }
     }
-    if (res == kResNew && s_bsz[lbk] + nnew >= B) bad = true;
-    if (bad) atomicMin(&s_cnt[lbk], r);
+    s_cnt[bk] = stop;
   }
   lds_barrier();
 

@@ -112,6 +112,38 @@ def test_single_run_repeat_fold(op, strategy, scores, ignore):
     assert p.g.load_factor() > 0.95
 
 
+@pytest.mark.parametrize("op", ["insert_or_assign", "find_or_insert", "insert_and_evict"])
+def test_single_run_new_keys_sharing_empty_slots(op):
+    """Buckets filled to 100 of 128 slots, then batches of 8, 14 and 20 new
+    keys per bucket on the single-run route: long runs of full slots make new keys
+    of one call share their first EMPTY slot (a later key takes the next one
+    its window recorded), run past the slots their window recorded (the
+    serial lane), and fill buckets (the eviction kernel)."""
+    rng = np.random.default_rng(306)
+    cap = 1 << 16
+    p = Pair(cap, dim=4, strategy=O.LRU)
+    buckets = list(range(0, 512, 11))  # at most 24 per partition
+    fill = np.concatenate([keys_in_buckets(rng, 100, cap, b, b + 1) for b in buckets])
+    p.insert_or_assign(fill, rand_vals(rng, fill.size, 4), None, clock=3)
+    p.assert_same_state()
+    for r in range(3):
+        new = np.concatenate([keys_in_buckets(rng, 8 + 6 * r, cap, b, b + 1, exclude=fill)
+                              for b in buckets])
+        fill = np.concatenate([fill, new])
+        q = np.concatenate([new, rng.choice(fill, 200)])
+        q = q[rng.permutation(q.size)]
+        v = rand_vals(rng, q.size, 4)
+        if op == "insert_or_assign":
+            p.insert_or_assign(q, v, None, unique_key=False, clock=10 + r)
+        elif op == "find_or_insert":
+            ov, gv = p.find_or_insert(q, v, None, unique_key=False, clock=10 + r)
+            np.testing.assert_array_equal(gv.view(np.uint8), ov.view(np.uint8))
+        else:
+            o, g = p.insert_and_evict(q, v, None, unique_key=False, clock=10 + r)
+            records_equal(o, g)
+        p.assert_same_state()
+
+
 @pytest.mark.parametrize("unique", [True, False])
 def test_single_run_find_or_insert_reads_same_batch_rows(unique):
     """find_or_insert with keys repeated in a batch: the later occurrences
