@@ -3000,6 +3000,79 @@ __device__ __forceinline__ void emit_fast(const TableView& t, const ApplyArgs& a
   }
 }
 
+// emit_fast for the buckets the parallel pass applied whole (serial flag 0),
+// by whole waves that take 64-entry chunks from the LDS counter *next (zero
+// beforehand): the waves that ran serial lanes join when those are done, so
+// every wave of the block copies rows.
+template <int OP, int U, bool kMovesRows>
+__device__ __forceinline__ void emit_fast_dyn(const TableView& t, const ApplyArgs& a, uint32_t m,
+                                              uint64_t part_b0, const uint64_t* s_key,
+                                              const uint32_t* s_idx, const uint64_t* s_sc,
+                                              const uint8_t* s_slot, const uint8_t* s_fl,
+                                              const uint32_t* s_off, const uint32_t* s_cnt,
+                                              const uint8_t* s_isser, uint32_t* s_rows,
+                                              uint32_t* next) {
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t B = t.B;
+  const uint64_t R64 = t.row_bytes;
+  for (;;) {
+    uint32_t c = 0;
+    if (lane == 0) c = atomicAdd(next, 1u);
+    c = __shfl(c, 0, 64);
+    if (c * 64 >= m) break;  // wave-uniform
+    const uint32_t e = c * 64 + lane;
+    uint64_t k = 0, h = 0, gb = 0;
+    uint32_t f = 0, tk = 0;
+    if (e < m) {
+      k = s_key[e];
+      h = murmur3(k);
+      gb = global_idx(t, h) >> t.bshift;
+      const uint32_t lbk = (uint32_t)(gb % kPartBuckets);
+      if (s_isser[lbk] == 0 && e - s_off[lbk] < s_cnt[lbk]) {
+        f = s_fl[e] & kMetaMask;
+        tk = s_fl[e] & kTkMask;
+      }
+    }
+    if (kMovesRows) {
+      uint64_t src = 0, dst = 0, asrc = 0, adst = 0;
+      if (tk) {
+        const uint64_t i = s_idx[e];
+        const uint32_t sl = s_slot[e];
+        const uint64_t trow = (uint64_t)(uintptr_t)row_ptr(t, gb, sl);
+        if (tk == kTkIn) {
+          src = (uint64_t)(uintptr_t)(a.in_values + i * R64);
+          dst = trow;
+        } else if (tk == kTkOut && OP == OP_ACCUM_OR_ASSIGN) {
+          asrc = (uint64_t)(uintptr_t)(a.in_values + i * R64);  // kTkAcc
+          adst = trow;
+        } else if (tk == kTkOut) {
+          src = trow;
+          dst = (uint64_t)(uintptr_t)(a.io_values + i * R64);
+        } else {
+          // The latest earlier key of the bucket whose input row was queued
+          // for this slot.
+          uint32_t xs = e;
+          for (uint32_t x = s_off[gb % kPartBuckets]; x < e; x++)
+            if (s_slot[x] == sl && (s_fl[x] & kTkMask) == kTkIn) xs = x;
+          src = (uint64_t)(uintptr_t)(a.io_values + (uint64_t)s_idx[xs] * R64);
+          dst = (uint64_t)(uintptr_t)(a.io_values + i * R64);
+        }
+      }
+      wave_copy_pairs_q<U, 4>(src, dst, t.row_bytes, s_rows);
+      if (OP == OP_ACCUM_OR_ASSIGN) wave_accum_pairs<U>(asrc, adst, t.row_bytes, a.value_type, s_rows);
+    }
+    if (f) {
+      const uint64_t s = gb * B + s_slot[e];
+      if (f == kMetaKey) {
+        slot_store(t, s, k, s_sc[e]);
+        G(t.digests)[s] = (uint8_t)key_digest(h);
+      } else {
+        slot_score(t, s) = s_sc[e];
+      }
+    }
+  }
+}
+
 template <int OP, int U>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_apply_fast(TableView t, ApplyArgs a, PartScratch ps) {
   constexpr uint32_t kPer = (kFastLds + kBlock - 1) / kBlock;  // entries per thread
@@ -3028,6 +3101,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
   __shared__ uint8_t s_serial[kPartBuckets];  // buckets left to the serial lanes
   __shared__ uint8_t s_isser[kPartBuckets];   // 1 for those buckets
   __shared__ uint32_t s_nser;
+  __shared__ uint32_t s_enext;  // next 64-entry chunk of the emit
   __shared__ uint32_t s_rbase, s_pbase;
   const uint32_t tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const uint32_t p = blockIdx.x;
@@ -3098,6 +3172,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
       s_nrec = 0;
       s_npool = 0;
       s_nser = 0;
+      s_enext = 0;
     }
     lds_barrier();
 #pragma unroll
@@ -3396,13 +3471,10 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
   lds_barrier();
   // The waves that hold serial lanes run them; meanwhile the other waves write
   // the records and copy the rows of the buckets the parallel pass applied
-  // whole (different buckets, so neither touches what the other reads).
+  // whole (different buckets, so neither touches what the other reads), in
+  // 64-entry chunks from a counter that the serial waves join when done.
   const uint32_t ns_w = (s_nser + 63) / 64;
-  if (wv >= ns_w) {
-    emit_fast<OP, U, moves_rows>(t, a, m, part_b0, (wv - ns_w) * 64 + lane, (kBlock / 64 - ns_w) * 64,
-                             0, s_key, s_idx, s_sc, s_slot, s_fl, s_off, s_cnt, s_isser,
-                             s_rows[wv]);
-  } else if (tid < s_nser) {
+  if (tid < s_nser) {
     const uint32_t bk = s_serial[tid];
     const uint64_t b = part_b0 + bk;
     const uint32_t lo = s_off[bk], hi = s_off[bk + 1], c = hi - lo;
@@ -3585,6 +3657,9 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
       added += bsz - s_bsz[bk];
     }
   }
+  if (ns_w < kBlock / 64)
+    emit_fast_dyn<OP, U, moves_rows>(t, a, m, part_b0, s_key, s_idx, s_sc, s_slot, s_fl, s_off,
+                                     s_cnt, s_isser, s_rows[wv], &s_enext);
   lds_barrier();
 
   /* W. Records and rows of the serial buckets; also of the others when
