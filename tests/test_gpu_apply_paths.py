@@ -144,6 +144,25 @@ def test_single_run_new_keys_sharing_empty_slots(op):
         p.assert_same_state()
 
 
+@pytest.mark.parametrize("n", [8 * 1024, 9 * 1024 + 37, 17 * 1024 - 5])
+def test_chunk_counts_around_the_xcd_mapping(n):
+    """Batch chunks (1024 keys) are counted and scattered by blocks that take
+    contiguous chunk ranges per XCD for the first 8 * floor(chunks / 8)
+    chunks and their own index after that: batches of 8, 10 and 17 chunks,
+    inserted and then found, against the oracle."""
+    rng = np.random.default_rng(307)
+    cap = 1 << 17
+    p = Pair(cap, dim=4, strategy=O.CUSTOMIZED)
+    for r in range(3):
+        ks = uniform_keys(rng, n)
+        sc = rng.integers(0, 1 << 30, n, dtype=np.uint64)
+        p.insert_or_assign(ks, rand_vals(rng, n, 4), sc, clock=5 + r)
+        ov, gv = p.find_or_insert(ks[rng.permutation(n)], rand_vals(rng, n, 4),
+                                  rng.integers(0, 1 << 30, n, dtype=np.uint64), clock=9 + r)
+        np.testing.assert_array_equal(gv.view(np.uint8), ov.view(np.uint8))
+        p.assert_same_state()
+
+
 @pytest.mark.parametrize("unique", [True, False])
 def test_single_run_find_or_insert_reads_same_batch_rows(unique):
     """find_or_insert with keys repeated in a batch: the later occurrences
