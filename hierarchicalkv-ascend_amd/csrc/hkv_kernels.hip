@@ -1006,11 +1006,20 @@ __device__ __forceinline__ bool lane_step(const TableView& t, const ApplyArgs& a
 //    chunk order, so all keys of segment g precede those of g + 1 in batch
 //    order.
 // 3. k_pscatter: every key writes {key, batch index} into its segment.
-// 4. k_apply_part: one workgroup per partition.  It loads the partition's
-//    entries into LDS (in runs of whole segments when they do not fit at
-//    once), groups them by bucket, and applies each bucket's keys in batch
-//    order: first one lane per bucket while no eviction is needed, then one
-//    16-lane group per bucket that needs the eviction path or holds many keys.
+// 4. k_apply_fast: one workgroup per partition of at most kFastLds entries,
+//    key-parallel with batch-order results; buckets that need the eviction
+//    path go to k_apply_deferred(_q) (one 16-lane group per bucket), larger
+//    partitions and buckets with more than kLaneMax keys to k_apply_part.
+// 5. k_apply_part: one workgroup per listed partition, taken from a counter.
+//    It folds the heavy buckets' repeated keys, then loads the other entries
+//    into LDS (in runs of whole segments when they do not fit at once),
+//    groups them by bucket and applies each bucket's keys in batch order:
+//    one lane per bucket while no eviction is needed, then one 16-lane group
+//    per bucket that needs the eviction path or holds many keys.
+//    k_big_count / k_big_fold / k_big_tasks do its per-entry passes over the
+//    whole GPU for the largest partitions of batches with repeated keys.
+// 6. find_or_insert's per-occurrence row copies (k_rowtasks) and
+//    insert_and_evict's record compaction (k_evc_*).
 // No atomics touch table memory: a bucket has exactly one owner at a time.
 
 constexpr uint32_t kPartLds = kPartChunk;  // entries one LDS load holds
