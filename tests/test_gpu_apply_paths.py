@@ -144,6 +144,39 @@ def test_single_run_new_keys_sharing_empty_slots(op):
         p.assert_same_state()
 
 
+@pytest.mark.parametrize("op", ["insert_or_assign", "find_or_insert"])
+@pytest.mark.parametrize("strategy", [O.LFU, O.EPOCH_LFU, O.CUSTOMIZED])
+def test_single_run_key_repeated_up_to_32(op, strategy):
+    """A key repeated 20 to 32 times in one bucket of the single-run route
+    (at most 32 keys per bucket, so no long-bucket split): the fold of its
+    scores (EpochLfu inputs near 2^31 saturate the low word) and its rows,
+    new and present keys, against the oracle."""
+    rng = np.random.default_rng(308 + strategy)
+    cap = 1 << 16
+    p = Pair(cap, dim=4, strategy=strategy)
+    p.set_global_epoch(4)
+    present = uniform_keys(rng, 2000)
+    p.insert_or_assign(present, rand_vals(rng, present.size, 4),
+                       rng.integers(1, 1 << 20, present.size, dtype=np.uint64), clock=2)
+    for r in range(4):
+        hot = np.concatenate([rng.choice(present, 6, replace=False),
+                              uniform_keys(rng, 6, exclude=present)])
+        reps = rng.integers(20, 33, hot.size)
+        q = np.concatenate([np.repeat(hot, reps), rng.choice(present, 300),
+                            uniform_keys(rng, 200, exclude=np.concatenate([present, hot]))])
+        q = q[rng.permutation(q.size)]
+        hi = (1 << 31) if strategy == O.EPOCH_LFU else (1 << 20)
+        sc = rng.integers(1, hi, q.size, dtype=np.uint64)
+        v = rand_vals(rng, q.size, 4)
+        if op == "insert_or_assign":
+            p.insert_or_assign(q, v, sc, unique_key=False, clock=20 + r)
+        else:
+            ov, gv = p.find_or_insert(q, v, sc, unique_key=False, clock=20 + r)
+            np.testing.assert_array_equal(gv.view(np.uint8), ov.view(np.uint8))
+        p.assert_same_state()
+        present = np.unique(np.concatenate([present, q]))
+
+
 @pytest.mark.parametrize("n", [8 * 1024, 9 * 1024 + 37, 17 * 1024 - 5])
 def test_chunk_counts_around_the_xcd_mapping(n):
     """Batch chunks (1024 keys) are counted and scattered by blocks that take
