@@ -2936,6 +2936,40 @@ __device__ __forceinline__ void wave_accum_pairs(uint64_t src, uint64_t dst, uin
   __builtin_amdgcn_wave_barrier();
 }
 
+// Does entry e carry a record or (pointer find_or_insert) a slot word?
+template <int OP>
+__device__ __forceinline__ bool emits_meta(uint8_t fl) {
+  if (fl & kMetaMask) return true;
+  const uint32_t res = fl & kResMask;
+  return OP == OP_FIND_OR_INSERT_PTR && (res == kResNew || res == kResDup);
+}
+
+// The metadata record of entry e at global slot s.  The pointer
+// find_or_insert also writes every applied key's slot word (slot + 1, found
+// flag) and, with unique keys, holds the slot LOCKED for the rest of the
+// batch, as the reference does.
+template <int OP>
+__device__ __forceinline__ void emit_record(const TableView& t, const ApplyArgs& a, uint32_t e,
+                                            uint64_t k, uint64_t h, uint64_t s,
+                                            const uint32_t* s_idx, const uint64_t* s_sc,
+                                            const uint8_t* s_fl) {
+  const uint8_t fl = s_fl[e];
+  const uint32_t f = fl & kMetaMask;
+  const bool lk = OP == OP_FIND_OR_INSERT_PTR && a.lock;
+  const bool dup = (fl & kResMask) == kResDup;
+  if (f == kMetaKey) {
+    slot_store(t, s, lk ? kLockedKey : k, s_sc[e]);
+    G(t.digests)[s] = (uint8_t)key_digest(h);
+  } else if (f == kMetaScore) {
+    if (lk) slot_store(t, s, kLockedKey, s_sc[e]);
+    else slot_score(t, s) = s_sc[e];
+  } else if (lk && dup) {
+    slot_key(t, s) = kLockedKey;
+  }
+  if (OP == OP_FIND_OR_INSERT_PTR && emits_meta<OP>(fl))
+    G(a.slot_out)[s_idx[e]] = (s + 1) | (dup ? kSlotFound : 0ull);
+}
+
 // Metadata records (at most one per slot) and row copies of the entries of a
 // k_apply_fast block whose bucket's serial flag equals `ser` (2: every
 // bucket), by the threads
@@ -2953,21 +2987,14 @@ __device__ __forceinline__ void emit_fast(const TableView& t, const ApplyArgs& a
                                           const uint8_t* s_isser, uint32_t* s_rows) {
   const uint32_t B = t.B;
   for (uint32_t e = t0; e < m; e += nthr) {
-    const uint32_t f = s_fl[e] & kMetaMask;
-    if (!f) continue;
+    if (!emits_meta<OP>(s_fl[e])) continue;
     const uint64_t k = s_key[e];
     const uint64_t h = murmur3(k);
     const uint64_t gb = global_idx(t, h) >> t.bshift;
     const uint32_t lbk = (uint32_t)(gb % kPartBuckets);
     if (ser != 2 && s_isser[lbk] != ser) continue;
     if (e - s_off[lbk] >= s_cnt[lbk]) continue;  // left to k_apply_deferred
-    const uint64_t s = gb * B + s_slot[e];
-    if (f == kMetaKey) {
-      slot_store(t, s, k, s_sc[e]);
-      G(t.digests)[s] = (uint8_t)key_digest(h);
-    } else {
-      slot_score(t, s) = s_sc[e];
-    }
+    emit_record<OP>(t, a, e, k, h, gb * B + s_slot[e], s_idx, s_sc, s_fl);
   }
   if (!kMovesRows) return;
   const uint64_t R64 = t.row_bytes;
@@ -3031,14 +3058,15 @@ __device__ __forceinline__ void emit_fast_dyn(const TableView& t, const ApplyArg
     if (c * 64 >= m) break;  // wave-uniform
     const uint32_t e = c * 64 + lane;
     uint64_t k = 0, h = 0, gb = 0;
-    uint32_t f = 0, tk = 0;
+    bool f = false;
+    uint32_t tk = 0;
     if (e < m) {
       k = s_key[e];
       h = murmur3(k);
       gb = global_idx(t, h) >> t.bshift;
       const uint32_t lbk = (uint32_t)(gb % kPartBuckets);
       if (s_isser[lbk] == 0 && e - s_off[lbk] < s_cnt[lbk]) {
-        f = s_fl[e] & kMetaMask;
+        f = emits_meta<OP>(s_fl[e]);
         tk = s_fl[e] & kTkMask;
       }
     }
@@ -3070,24 +3098,18 @@ __device__ __forceinline__ void emit_fast_dyn(const TableView& t, const ApplyArg
       wave_copy_pairs_q<U, 4>(src, dst, t.row_bytes, s_rows);
       if (OP == OP_ACCUM_OR_ASSIGN) wave_accum_pairs<U>(asrc, adst, t.row_bytes, a.value_type, s_rows);
     }
-    if (f) {
-      const uint64_t s = gb * B + s_slot[e];
-      if (f == kMetaKey) {
-        slot_store(t, s, k, s_sc[e]);
-        G(t.digests)[s] = (uint8_t)key_digest(h);
-      } else {
-        slot_score(t, s) = s_sc[e];
-      }
-    }
+    if (f) emit_record<OP>(t, a, e, k, h, gb * B + s_slot[e], s_idx, s_sc, s_fl);
   }
 }
 
 template <int OP, int U>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_apply_fast(TableView t, ApplyArgs a, PartScratch ps) {
   constexpr uint32_t kPer = (kFastLds + kBlock - 1) / kBlock;  // entries per thread
-  constexpr bool kSplitLong = OP != OP_ACCUM_OR_ASSIGN;
+  // accum_or_assign and the pointer find_or_insert list a partition with a
+  // long bucket whole (k_apply_part and k_apply_seq take it).
+  constexpr bool kSplitLong = OP != OP_ACCUM_OR_ASSIGN && OP != OP_FIND_OR_INSERT_PTR;
   constexpr bool may_insert = OP != OP_ASSIGN_SCORES;
-  constexpr bool moves_rows = OP != OP_ASSIGN_SCORES;
+  constexpr bool moves_rows = OP != OP_ASSIGN_SCORES && OP != OP_FIND_OR_INSERT_PTR;
   constexpr bool reads_rows = OP == OP_FIND_OR_INSERT;
   // Entries of the partition, grouped by bucket and in batch order inside a
   // bucket: the rank of entry e of bucket [lo, hi) in the batch is e - lo.
@@ -3518,6 +3540,17 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
       const uint32_t e = lo + r;
       const uint64_t k = s_key[e];
       const uint64_t i = s_idx[e];
+      if (OP == OP_FIND_OR_INSERT_PTR && a.lock) {
+        // A key met again while its earlier slot is held LOCKED matches
+        // nothing there: the eviction kernel, which reads the bucket back
+        // with the lock in place, applies the rest of the bucket.
+        bool again = false;
+        for (uint32_t x = lo; x < e; x++) again |= s_key[x] == k;
+        if (again) {
+          stop = r;
+          break;
+        }
+      }
       const uint64_t in = has_in ? G(a.in_scores)[i] : 0;
       const uint64_t h = murmur3(k);
       const uint32_t start = (uint32_t)(global_idx(t, h) & (B - 1));
@@ -4072,8 +4105,10 @@ k_apply_deferred_q(TableView t, ApplyArgs a, PartScratch ps) {
 /* pointer APIs: find*, find_and_update, find_or_insert*, lock / unlock      */
 /* ------------------------------------------------------------------------ */
 
-// Placement of the pointer find_or_insert: every partition, each bucket's
-// keys in batch order through apply_key, one 16-lane group per bucket.  A
+// Placement of the pointer find_or_insert for the partitions k_apply_fast
+// lists (more entries than one LDS load, or a bucket with more than kLaneMax
+// keys): each bucket's keys in batch order through apply_key, one 16-lane
+// group per bucket.  A
 // partition's entries load in runs that end at a chunk boundary (one chunk's
 // entries of a partition are contiguous but unordered), so that a bucket's
 // keys in one run all precede its keys in the next.
@@ -4093,11 +4128,14 @@ __global__ __launch_bounds__(kBlock) void k_apply_seq(TableView t, ApplyArgs a, 
   const uint32_t tid = threadIdx.x, gl = tid & 15;
   gptr<const u64x2> ent = G(reinterpret_cast<const u64x2*>(ps.ent));
   int32_t added = 0;  // keys this lane's buckets gained
+  const uint32_t nlist = *(volatile uint32_t*)&ps.dctr[2];
+  if (nlist == 0) return;
   for (;;) {
     if (tid == 0) s_li = atomicAdd(&ps.dctr[3], 1u);
     __syncthreads();
-    const uint32_t p = s_li;
-    if (p >= ps.np) break;  // block-uniform
+    const uint32_t li = s_li;
+    if (li >= nlist) break;  // block-uniform
+    const uint32_t p = ps.plist[li];
     const uint32_t base_e = ps.pinfo[2 * p], m = ps.pinfo[2 * p + 1];
     const uint64_t part_b0 = (uint64_t)p * kPartBuckets;
     for (uint32_t r0 = 0; r0 < m;) {
@@ -4858,7 +4896,11 @@ void launch_find_or_insert_ptr(const TableView& t, const ApplyArgs& a0, const Pa
   hipLaunchKernelGGL(k_pcount, dim3(ps.chunks), dim3(kBlock), lds, s, t, a.keys, a.n, ps);
   hipLaunchKernelGGL(k_pscan, dim3((ps.np + kScanCols - 1) / kScanCols), dim3(1024), 0, s, ps);
   hipLaunchKernelGGL(k_pscatter, dim3(ps.chunks), dim3(kBlock), lds, s, t, a.keys, a.n, ps);
-  const dim3 gp(ps.np < 2048 ? ps.np : 2048), b(kBlock);
+  const dim3 g(ps.np), b(kBlock);
+  hipLaunchKernelGGL((k_apply_fast<OP_FIND_OR_INSERT_PTR, 16>), g, b, 0, s, t, a, ps);
+  hipLaunchKernelGGL((k_apply_deferred<OP_FIND_OR_INSERT_PTR, 16>),
+                     dim3(grid_for(a.n * 16, kBlock, 1024)), b, 0, s, t, a, ps);
+  const dim3 gp(ps.np < 256 ? ps.np : 256);
   hipLaunchKernelGGL((k_apply_seq<OP_FIND_OR_INSERT_PTR, 16>), gp, b, 0, s, t, a, ps);
   hipLaunchKernelGGL(k_ptr_finish, dim3(grid_for(a.n, kBlock, 1ull << 31)), b, 0, s, t, a.keys,
                      a.n, ps.trow, vptrs, founds, kptrs, (a.lock && !keep_locked) ? 1 : 0);

@@ -225,6 +225,56 @@ def test_find_or_insert_ptr_matches_oracle(strategy, unique, keep):
         assert_same_layout(g, o, np.unique(np.concatenate(every)))
 
 
+@pytest.mark.parametrize("strategy,unique,keep,dups", [
+    ("kCustomized", True, False, False), ("kCustomized", True, True, False),
+    ("kCustomized", False, False, True), ("kLfu", True, False, False),
+    ("kLfu", False, False, True), ("kLru", True, True, False), ("kEpochLfu", False, False, True),
+    ("kCustomized", True, False, True), ("kLfu", True, True, True)])
+def test_find_or_insert_ptr_single_run(strategy, unique, keep, dups):
+    """The pointer find_or_insert on a 512-bucket table with batches under
+    one LDS load per partition (the key-parallel single-run kernel): present
+    and new keys, repeats (also under unique_key, where a repeat must not
+    match the slot its earlier occurrence holds LOCKED), and a table filled
+    past full so that buckets go to the eviction kernel."""
+    torch, H = _mods()
+    st = getattr(H.EvictStrategy, strategy)
+    rng = np.random.default_rng(11)
+    dim = 8
+    cap = 1 << 16
+    g, o = make(st, cap, dim=dim)
+    if strategy == "kEpochLfu":
+        g.set_global_epoch(5)
+        o.set_global_epoch(5)
+    uses = strategy != "kLru"
+    base = uniform_keys(rng, 60000)
+    insert_both(g, o, base, dim, rng.integers(1, 1 << 30, size=base.size, dtype=np.uint64)
+                if uses else None)
+    every = [base]
+    for r in range(4):
+        ks = np.concatenate([rng.choice(base, 400, replace=False), uniform_keys(rng, 800)])
+        if dups:
+            ks[900:1000] = ks[:100]  # repeats within the batch
+        ks = ks[rng.permutation(ks.size)]
+        sc = rng.integers(1, 1 << 30, size=ks.size, dtype=np.uint64) if uses else None
+        clk = 2000 + r
+        g.set_lru_clock(clk)
+        vp, fd, kp = _foi_ptr(g, ks, sc, unique, keep)
+        oslots, ofound = o.find_or_insert_ptr(ks, sc, unique_key=unique,
+                                              keep_locked=keep, clock=clk)
+        np.testing.assert_array_equal(fd, ofound)
+        ek, ev = expected_ptrs(g, oslots)
+        np.testing.assert_array_equal(vp, ev)
+        if keep:
+            np.testing.assert_array_equal(kp, ek)
+            torch_ok = torch.zeros(ks.size, dtype=torch.uint8, device="cuda")
+            g.unlock_keys(ks.size, to_dev(kp), to_dev(ks), torch_ok)
+            torch.cuda.synchronize()
+            ook = o.unlock_keys(oslots, ks)
+            np.testing.assert_array_equal(to_np(torch_ok, np.uint8).astype(bool), ook)
+        every.append(ks)
+        assert_same_layout(g, o, np.unique(np.concatenate(every)))
+
+
 def test_rows_written_through_pointers():
     # The reference's find_or_insert_safe_ptr pattern
     # (tests/community/find_or_insert_ptr_lock_test.cpp:152-169): rows of
