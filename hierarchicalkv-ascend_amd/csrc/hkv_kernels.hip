@@ -2747,6 +2747,7 @@ constexpr uint8_t kResDup = 2 << 4;   // present at the slot
 constexpr uint8_t kResSlow = 3 << 4;  // undecided by the window (or needs the serial lane)
 constexpr uint8_t kResMask = 3 << 4;
 constexpr uint8_t kRepeat = 1 << 6;  // a later occurrence of a key met earlier in its bucket
+constexpr uint8_t kRest = 1 << 7;    // assign_scores: the window held neither the key nor an EMPTY slot
 
 __device__ __forceinline__ uint32_t sel4(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3,
                                          uint32_t q) {
@@ -3371,13 +3372,73 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
           sc = score_new(a.sc, has_in, in, des, 0, &w);
           fl = kResNew | kMetaKey | kTkIn;
         }
+      } else if (OP == OP_ASSIGN_SCORES && !wp[q].over) {
+        fl = kResSlow | kRest;  // step B2 reads the rest of the bucket
       }
       s_slot[e] = slot;
 #pragma unroll
       for (uint32_t j = 0; j < kMoreEmpty; j++)
         s_more[j][e] = wp[q].more[j] != kNone ? (uint8_t)wp[q].more[j] : kNoSlot;
       s_fl[e] = fl;
-      if (fl != kResSlow) s_sc[e] = sc;
+      if ((fl & kResMask) != kResSlow) s_sc[e] = sc;
+    }
+    /* B2 (assign_scores).  A key whose window (two 16-slot chunks) held
+           neither the key nor an EMPTY slot: the rest of its bucket's
+           digest line in probe order (the other six chunks, then the start
+           chunk's groups before the start's group).  Up to two digest matches
+           before the first EMPTY slot are checked with one 16-byte record
+           load each; the key is then present at a match or absent (a no-op),
+           and only more matches leave it to the serial lane. */
+    if (OP == OP_ASSIGN_SCORES) {
+#pragma unroll 1
+      for (uint32_t q = 0; q < kPer; q++) {
+        const uint32_t e = tid + q * kBlock;
+        if (e >= m || !(s_fl[e] & kRest)) continue;
+        const uint64_t k = s_key[e];
+        const uint64_t h = murmur3(k);
+        const uint64_t g2 = global_idx(t, h);
+        const uint32_t ch = (uint32_t)(g2 & (B - 1)) >> 4;
+        const uint64_t base = (g2 >> t.bshift) * B;
+        gptr<const u32x4> drow = (gptr<const u32x4>)(G(t.digests) + base);
+        // The six chunks after the window, then the groups of the start's
+        // chunk before the start's group (last in probe order).
+        u32x4 w7[7];
+#pragma unroll
+        for (uint32_t c = 0; c < 7; c++) w7[c] = drow[(ch + 2 + c) & (B / 16 - 1)];
+        const uint32_t g0 = ((uint32_t)(g2 & (B - 1)) >> 2) & 3u;
+        const uint32_t rep = key_digest(h) * 0x01010101u;
+        WinProbe r{0, kNone, kNone, {kNone}, 0, false, false};
+#pragma unroll
+        for (uint32_t c = 0; c < 7; c++) {
+          const uint32_t cb = ((ch + 2 + c) & (B / 16 - 1)) * 16;
+          const uint32_t ng = c < 6 ? 4u : g0;  // groups of this chunk in the rest
+          if (ng > 0) probe_group(r, w7[c].x, cb, rep, 0xFu);
+          if (ng > 1) probe_group(r, w7[c].y, cb + 4, rep, 0xFu);
+          if (ng > 2) probe_group(r, w7[c].z, cb + 8, rep, 0xFu);
+          if (ng > 3) probe_group(r, w7[c].w, cb + 12, rep, 0xFu);
+        }
+        uint8_t fl = kResSlow;
+        uint8_t slot = kNoSlot;
+        if (!r.over) {
+          const u64x2 r0 = r.c0 != kNone ? slot_load(t, base + r.c0) : u64x2{0, 0};
+          const u64x2 r1 = r.c1 != kNone ? slot_load(t, base + r.c1) : u64x2{0, 0};
+          const bool h0 = r.c0 != kNone && r0.x == k;
+          const bool h1 = !h0 && r.c1 != kNone && r1.x == k;
+          if (h0 || h1) {
+            const uint64_t in = s_sc[e];
+            const uint64_t old = h0 ? r0.y : r1.y;
+            bool w;
+            const uint64_t ns = score_wo_missed(a.sc, has_in, in, old, &w);
+            slot = (uint8_t)(h0 ? r.c0 : r.c1);
+            fl = kResDup | (w ? kMetaScore : 0);
+            s_sc[e] = ns;
+          } else {
+            fl = 0;  // absent: a no-op
+          }
+        }
+        s_slot[e] = slot;
+        s_fl[e] = fl;
+      }
     }
   }
   lds_barrier();

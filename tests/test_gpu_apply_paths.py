@@ -177,6 +177,33 @@ def test_single_run_key_repeated_up_to_32(op, strategy):
         present = np.unique(np.concatenate([present, q]))
 
 
+@pytest.mark.parametrize("strategy", [O.LRU, O.LFU, O.EPOCH_LRU, O.EPOCH_LFU, O.CUSTOMIZED])
+def test_single_run_assign_scores_full_buckets(strategy):
+    """assign_scores on a table filled past full, on the single-run route:
+    present keys anywhere in their bucket (also past the probe window and in
+    the start chunk's groups before the start) take their new scores, absent
+    keys change nothing, whether or not the bucket has an EMPTY slot."""
+    rng = np.random.default_rng(309 + strategy)
+    cap = 1 << 16
+    p = Pair(cap, dim=4, strategy=strategy)
+    p.set_global_epoch(3)
+    uses = strategy not in (O.LRU, O.EPOCH_LRU)
+    keys = uniform_keys(rng, 90000)
+    for b in range(0, keys.size, 9000):
+        ks = keys[b:b + 9000]
+        p.insert_or_assign(ks, rand_vals(rng, ks.size, 4),
+                           rng.integers(1, 1 << 30, ks.size, dtype=np.uint64) if uses else None,
+                           clock=5 + b)
+    p.assert_same_state()
+    for r in range(3):
+        q = np.concatenate([rng.choice(keys, 600, replace=False),
+                            uniform_keys(rng, 600, exclude=keys)])
+        q = q[rng.permutation(q.size)]
+        sc = rng.integers(1, 1 << 31, q.size, dtype=np.uint64) if uses else None
+        p.assign_scores(q, sc, clock=100 + r)
+        p.assert_same_state()
+
+
 @pytest.mark.parametrize("n", [8 * 1024, 9 * 1024 + 37, 17 * 1024 - 5])
 def test_chunk_counts_around_the_xcd_mapping(n):
     """Batch chunks (1024 keys) are counted and scattered by blocks that take
