@@ -2747,7 +2747,7 @@ constexpr uint8_t kResDup = 2 << 4;   // present at the slot
 constexpr uint8_t kResSlow = 3 << 4;  // undecided by the window (or needs the serial lane)
 constexpr uint8_t kResMask = 3 << 4;
 constexpr uint8_t kRepeat = 1 << 6;  // a later occurrence of a key met earlier in its bucket
-constexpr uint8_t kRest = 1 << 7;    // assign_scores: the window held neither the key nor an EMPTY slot
+constexpr uint8_t kRest = 1 << 7;    // the window held neither the key nor an EMPTY slot (step B2)
 
 __device__ __forceinline__ uint32_t sel4(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3,
                                          uint32_t q) {
@@ -3163,6 +3163,13 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
   const bool has_in = a.in_scores != nullptr;
   const bool old_for_hit = a.sc.strategy == kLfu || a.sc.strategy == kEpochLfu;
   const bool old_for_new = a.sc.strategy == kLfu && !has_in;
+  // Step B2 runs for assign_scores, and on full buckets for insert_and_evict
+  // and accum_or_assign, whose handed-over buckets take the queued eviction
+  // kernel: a present key past its window is decided here instead of sending
+  // its bucket there.  For the other upserts the scan measured slower on a
+  // full table of new keys, which all go to the eviction path anyway.
+  constexpr bool kRestScan = OP == OP_ASSIGN_SCORES || OP == OP_INSERT_AND_EVICT ||
+                             OP == OP_ACCUM_OR_ASSIGN;
   // Batches with repeated keys: a key's later occurrences in its bucket are
   // applied beside its first one (step F), with the scores folded as the
   // sequential updates would leave them.  The fold needs the input scores of
@@ -3372,7 +3379,9 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
           sc = score_new(a.sc, has_in, in, des, 0, &w);
           fl = kResNew | kMetaKey | kTkIn;
         }
-      } else if (OP == OP_ASSIGN_SCORES && !wp[q].over) {
+      } else if (kRestScan && !wp[q].over &&
+                 (OP == OP_ASSIGN_SCORES ||
+                  s_bsz[(uint32_t)((gi[q] >> t.bshift) % kPartBuckets)] >= B)) {
         fl = kResSlow | kRest;  // step B2 reads the rest of the bucket
       }
       s_slot[e] = slot;
@@ -3382,14 +3391,17 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
       s_fl[e] = fl;
       if ((fl & kResMask) != kResSlow) s_sc[e] = sc;
     }
-    /* B2 (assign_scores).  A key whose window (two 16-slot chunks) held
-           neither the key nor an EMPTY slot: the rest of its bucket's
-           digest line in probe order (the other six chunks, then the start
-           chunk's groups before the start's group).  Up to two digest matches
-           before the first EMPTY slot are checked with one 16-byte record
-           load each; the key is then present at a match or absent (a no-op),
-           and only more matches leave it to the serial lane. */
-    if (OP == OP_ASSIGN_SCORES) {
+    /* B2 (kRestScan).  A key whose window (two 16-slot chunks) held neither
+           the key nor an EMPTY slot, in a full bucket (or for assign_scores,
+           in any):
+           the rest of its bucket's digest line in probe order (the other six
+           chunks, then the start chunk's groups before the start's group).
+           Up to two digest matches before the first EMPTY slot are checked
+           with one 16-byte record load each; the key is then present at a
+           match, or absent (a no-op for assign_scores and for an accumulation,
+           the eviction path for the others), and only more matches leave it
+           to the serial lane. */
+    if (kRestScan) {
 #pragma unroll 1
       for (uint32_t q = 0; q < kPer; q++) {
         const uint32_t e = tid + q * kBlock;
@@ -3424,15 +3436,25 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
           const u64x2 r1 = r.c1 != kNone ? slot_load(t, base + r.c1) : u64x2{0, 0};
           const bool h0 = r.c0 != kNone && r0.x == k;
           const bool h1 = !h0 && r.c1 != kNone && r1.x == k;
+          const bool acc_flag = OP == OP_ACCUM_OR_ASSIGN && G(a.accum_flags)[s_idx[e]] != 0;
           if (h0 || h1) {
-            const uint64_t in = s_sc[e];
-            const uint64_t old = h0 ? r0.y : r1.y;
-            bool w;
-            const uint64_t ns = score_wo_missed(a.sc, has_in, in, old, &w);
-            slot = (uint8_t)(h0 ? r.c0 : r.c1);
-            fl = kResDup | (w ? kMetaScore : 0);
-            s_sc[e] = ns;
-          } else {
+            if (OP == OP_ACCUM_OR_ASSIGN && !acc_flag) {
+              fl = 0;  // present, assign requested: a no-op
+            } else {
+              const uint64_t in = s_sc[e];
+              const uint64_t old = h0 ? r0.y : r1.y;
+              bool w;
+              const uint64_t ns =
+                  OP == OP_ASSIGN_SCORES
+                      ? score_wo_missed(a.sc, has_in, in, old, &w)
+                      : score_hit(a.sc, has_in, in, score_desired(a.sc, has_in, in), old, &w);
+              slot = (uint8_t)(h0 ? r.c0 : r.c1);
+              fl = kResDup | (w ? kMetaScore : 0);
+              if (OP == OP_ACCUM_OR_ASSIGN) fl |= kTkAcc;
+              else if (moves_rows) fl |= reads_rows ? kTkOut : kTkIn;
+              s_sc[e] = ns;
+            }
+          } else if (OP == OP_ASSIGN_SCORES || acc_flag) {
             fl = 0;  // absent: a no-op
           }
         }

@@ -177,12 +177,14 @@ def test_single_run_key_repeated_up_to_32(op, strategy):
         present = np.unique(np.concatenate([present, q]))
 
 
+@pytest.mark.parametrize("op", ["assign_scores", "insert_and_evict", "accum_or_assign"])
 @pytest.mark.parametrize("strategy", [O.LRU, O.LFU, O.EPOCH_LRU, O.EPOCH_LFU, O.CUSTOMIZED])
-def test_single_run_assign_scores_full_buckets(strategy):
-    """assign_scores on a table filled past full, on the single-run route:
-    present keys anywhere in their bucket (also past the probe window and in
-    the start chunk's groups before the start) take their new scores, absent
-    keys change nothing, whether or not the bucket has an EMPTY slot."""
+def test_single_run_full_buckets(op, strategy):
+    """assign_scores, insert_and_evict and accum_or_assign on a table filled
+    past full, on the single-run route: present keys anywhere in their
+    bucket (also past the probe window and in the start chunk's groups
+    before the start) are applied there, absent keys are no-ops
+    (assign_scores, accumulations) or take the eviction path."""
     rng = np.random.default_rng(309 + strategy)
     cap = 1 << 16
     p = Pair(cap, dim=4, strategy=strategy)
@@ -200,7 +202,15 @@ def test_single_run_assign_scores_full_buckets(strategy):
                             uniform_keys(rng, 600, exclude=keys)])
         q = q[rng.permutation(q.size)]
         sc = rng.integers(1, 1 << 31, q.size, dtype=np.uint64) if uses else None
-        p.assign_scores(q, sc, clock=100 + r)
+        if op == "assign_scores":
+            p.assign_scores(q, sc, clock=100 + r)
+        elif op == "insert_and_evict":
+            o, g = p.insert_and_evict(q, rand_vals(rng, q.size, 4), sc, clock=100 + r)
+            records_equal(o, g)
+        else:
+            flags = np.isin(q, keys)
+            flags[rng.random(q.size) < 0.2] ^= True  # some flags do not match
+            p.accum_or_assign(q, rand_vals(rng, q.size, 4) * 0.01, flags, sc, clock=100 + r)
         p.assert_same_state()
 
 
