@@ -1436,8 +1436,11 @@ int hkv_export_batch_if(hkv_table* t, int pred, uint64_t pattern, uint64_t thres
                         uint64_t* scores, hkv_stream stream) {
   return guarded([&] {
     need_table(t);
-    // include/hkv_hashtable.h:2623-2672
-    if (!d_counter || !keys || !values) fail(HKV_ERR_INVALID, "counter, keys and values must not be null");
+    // include/hkv_hashtable.h:2623-2672: the counter is cleared, and a window
+    // of no slots (n == 0, or offset at or past the capacity) returns there.
+    if (!d_counter) fail(HKV_ERR_INVALID, "d_counter must not be null");
+    const bool window = offset < t->C && n > 0;
+    if (window && (!keys || !values)) fail(HKV_ERR_INVALID, "keys and values must not be null");
     const hkv_device_view v = device_view(t);
     const bool wide = (t->row % 4) == 0 && ((uintptr_t)values % 4) == 0;
     ExportIfBody body{v, pattern, threshold, n, offset, reinterpret_cast<unsigned long long*>(d_counter),

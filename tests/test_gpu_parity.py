@@ -303,6 +303,50 @@ def test_reserved_keys_and_empty_batches():
     p.assert_same_state()
 
 
+def test_every_batch_api_with_zero_keys():
+    """n == 0 returns before any argument check, with null pointers, and
+    leaves the table and the caller's counters alone
+    (include/hkv_hashtable.h:1099, 1270, 2182); export_batch and
+    export_batch_if still clear their counter first (:2530, :2636)."""
+    import hkv_amd
+    import torch
+    rng = np.random.default_rng(115)
+    p = Pair(1 << 12, dim=4, strategy=O.CUSTOMIZED)
+    ks = uniform_keys(rng, 1500)
+    p.insert_or_assign(ks, rand_vals(rng, 1500, 4), rng.integers(1, 1000, 1500, dtype=np.uint64))
+    g = p.g
+    g.insert_or_assign(0, None, None, None)
+    g.insert_or_assign_noalloc(0, None, None, None)
+    cnt = torch.full((1,), 7, dtype=torch.int64, device="cuda")
+    g.insert_and_evict(0, None, None, None, None, None, None, d_evicted_counter=cnt)
+    assert g.insert_and_evict(0, None, None, None, None, None, None) == 0
+    g.accum_or_assign(0, None, None, None, None)
+    g.find_or_insert(0, None, None, None)
+    g.find_or_insert(0, None, None, None, unique_key=False)
+    g.assign_scores(0, None, None)
+    g.assign(0, None, None, None)
+    g.assign_values(0, None, None)
+    g.contains(0, None, None)
+    g.find(0, None, None, None)
+    ms = torch.full((1,), 5, dtype=torch.int32, device="cuda")
+    g.find_missed(0, None, None, None, None, ms)
+    g.find_ptr(0, None, None)
+    g.find_and_update(0, None, None)
+    g.find_or_insert_ptr(0, None, None, None)
+    g.lock_keys(0, None, None)
+    g.unlock_keys(0, None, None)
+    g.erase(0, None)
+    ec = torch.full((1,), 9, dtype=torch.int64, device="cuda")
+    g.export_batch(0, 0, None, None, None, d_counter=ec)
+    ei = torch.full((1,), 9, dtype=torch.int64, device="cuda")
+    g.export_batch_if(hkv_amd.PRED_SCORE_LT, 0, 0, 0, 0, ei, None, None)
+    torch.cuda.synchronize()
+    assert int(cnt.item()) == 7 and int(ms.item()) == 5
+    assert int(ec.item()) == 0 and int(ei.item()) == 0
+    assert g.size() == 1500
+    p.assert_same_state()
+
+
 @pytest.mark.parametrize("vt,dim", [("f32", 1), ("f32", 27), ("f32", 64),
                                     ("f32", 128), ("u8", 3), ("f16", 8),
                                     ("i64", 5), ("f64", 2)])
