@@ -2978,6 +2978,40 @@ __device__ __forceinline__ void emit_record(const TableView& t, const ApplyArgs&
 // Tasks of different keys name different rows (a superseded write was
 // dropped), except that a forwarded read takes an input row that is only
 // read, so they run in any order.
+// Source and destination rows of entry e's row task tk (bucket gb) in a
+// k_apply_fast block: a copy (src -> dst) or, for accum_or_assign, an
+// accumulation (asrc into adst).
+template <int OP>
+__device__ __forceinline__ void fast_row_task(const TableView& t, const ApplyArgs& a, uint32_t e,
+                                              uint64_t gb, uint32_t tk, const uint32_t* s_idx,
+                                              const uint8_t* s_slot, const uint8_t* s_fl,
+                                              const uint32_t* s_off, uint64_t& src,
+                                              uint64_t& dst, uint64_t& asrc, uint64_t& adst) {
+  const uint64_t R64 = t.row_bytes;
+  const uint64_t i = s_idx[e];
+  const uint32_t sl = s_slot[e];
+  const uint64_t trow = (uint64_t)(uintptr_t)row_ptr(t, gb, sl);
+  if (tk == kTkIn) {
+    src = (uint64_t)(uintptr_t)(a.in_values + i * R64);
+    dst = trow;
+  } else if (tk == kTkOut && OP == OP_ACCUM_OR_ASSIGN) {
+    asrc = (uint64_t)(uintptr_t)(a.in_values + i * R64);  // kTkAcc
+    adst = trow;
+  } else if (tk == kTkOut) {
+    src = trow;
+    dst = (uint64_t)(uintptr_t)(a.io_values + i * R64);
+  } else {
+    // The latest earlier key of the bucket whose input row was queued for
+    // this slot.
+    uint32_t xs = e;
+    for (uint32_t x = s_off[gb % kPartBuckets]; x < e; x++)
+      if (s_slot[x] == sl && (s_fl[x] & kTkMask) == kTkIn) xs = x;
+    src = (uint64_t)(uintptr_t)(a.io_values + (uint64_t)s_idx[xs] * R64);
+    dst = (uint64_t)(uintptr_t)(a.io_values + i * R64);
+  }
+}
+
+// With with_rows false only the metadata records are written.
 template <int OP, int U, bool kMovesRows>
 __device__ __forceinline__ void emit_fast(const TableView& t, const ApplyArgs& a, uint32_t m,
                                           uint64_t part_b0, uint32_t t0, uint32_t nthr,
@@ -2985,7 +3019,8 @@ __device__ __forceinline__ void emit_fast(const TableView& t, const ApplyArgs& a
                                           const uint32_t* s_idx, const uint64_t* s_sc,
                                           const uint8_t* s_slot, const uint8_t* s_fl,
                                           const uint32_t* s_off, const uint32_t* s_cnt,
-                                          const uint8_t* s_isser, uint32_t* s_rows) {
+                                          const uint8_t* s_isser, uint32_t* s_rows,
+                                          bool with_rows = true) {
   const uint32_t B = t.B;
   for (uint32_t e = t0; e < m; e += nthr) {
     if (!emits_meta<OP>(s_fl[e])) continue;
@@ -2997,8 +3032,7 @@ __device__ __forceinline__ void emit_fast(const TableView& t, const ApplyArgs& a
     if (e - s_off[lbk] >= s_cnt[lbk]) continue;  // left to k_apply_deferred
     emit_record<OP>(t, a, e, k, h, gb * B + s_slot[e], s_idx, s_sc, s_fl);
   }
-  if (!kMovesRows) return;
-  const uint64_t R64 = t.row_bytes;
+  if (!kMovesRows || !with_rows) return;
   for (uint32_t e0 = 0; e0 < m; e0 += nthr) {
     const uint32_t e = e0 + t0;
     uint64_t src = 0, dst = 0, asrc = 0, adst = 0;
@@ -3009,29 +3043,8 @@ __device__ __forceinline__ void emit_fast(const TableView& t, const ApplyArgs& a
       const uint32_t lbk = (uint32_t)(gb % kPartBuckets);
       if ((ser != 2 && s_isser[lbk] != ser) || e - s_off[lbk] >= s_cnt[lbk]) tk = 0;
     }
-    if (tk) {
-      const uint64_t i = s_idx[e];
-      const uint32_t sl = s_slot[e];
-      const uint64_t trow = (uint64_t)(uintptr_t)row_ptr(t, gb, sl);
-      if (tk == kTkIn) {
-        src = (uint64_t)(uintptr_t)(a.in_values + i * R64);
-        dst = trow;
-      } else if (tk == kTkOut && OP == OP_ACCUM_OR_ASSIGN) {
-        asrc = (uint64_t)(uintptr_t)(a.in_values + i * R64);  // kTkAcc
-        adst = trow;
-      } else if (tk == kTkOut) {
-        src = trow;
-        dst = (uint64_t)(uintptr_t)(a.io_values + i * R64);
-      } else {
-        // The latest earlier key of the bucket whose input row was queued
-        // for this slot.
-        uint32_t xs = e;
-        for (uint32_t x = s_off[gb % kPartBuckets]; x < e; x++)
-          if (s_slot[x] == sl && (s_fl[x] & kTkMask) == kTkIn) xs = x;
-        src = (uint64_t)(uintptr_t)(a.io_values + (uint64_t)s_idx[xs] * R64);
-        dst = (uint64_t)(uintptr_t)(a.io_values + i * R64);
-      }
-    }
+    if (tk)
+      fast_row_task<OP>(t, a, e, gb, tk, s_idx, s_slot, s_fl, s_off, src, dst, asrc, adst);
     wave_copy_pairs_q<U, 4>(src, dst, t.row_bytes, s_rows);
     if (OP == OP_ACCUM_OR_ASSIGN) wave_accum_pairs<U>(asrc, adst, t.row_bytes, a.value_type, s_rows);
   }
@@ -3051,7 +3064,6 @@ __device__ __forceinline__ void emit_fast_dyn(const TableView& t, const ApplyArg
                                               uint32_t* next) {
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t B = t.B;
-  const uint64_t R64 = t.row_bytes;
   for (;;) {
     uint32_t c = 0;
     if (lane == 0) c = atomicAdd(next, 1u);
@@ -3073,29 +3085,8 @@ __device__ __forceinline__ void emit_fast_dyn(const TableView& t, const ApplyArg
     }
     if (kMovesRows) {
       uint64_t src = 0, dst = 0, asrc = 0, adst = 0;
-      if (tk) {
-        const uint64_t i = s_idx[e];
-        const uint32_t sl = s_slot[e];
-        const uint64_t trow = (uint64_t)(uintptr_t)row_ptr(t, gb, sl);
-        if (tk == kTkIn) {
-          src = (uint64_t)(uintptr_t)(a.in_values + i * R64);
-          dst = trow;
-        } else if (tk == kTkOut && OP == OP_ACCUM_OR_ASSIGN) {
-          asrc = (uint64_t)(uintptr_t)(a.in_values + i * R64);  // kTkAcc
-          adst = trow;
-        } else if (tk == kTkOut) {
-          src = trow;
-          dst = (uint64_t)(uintptr_t)(a.io_values + i * R64);
-        } else {
-          // The latest earlier key of the bucket whose input row was queued
-          // for this slot.
-          uint32_t xs = e;
-          for (uint32_t x = s_off[gb % kPartBuckets]; x < e; x++)
-            if (s_slot[x] == sl && (s_fl[x] & kTkMask) == kTkIn) xs = x;
-          src = (uint64_t)(uintptr_t)(a.io_values + (uint64_t)s_idx[xs] * R64);
-          dst = (uint64_t)(uintptr_t)(a.io_values + i * R64);
-        }
-      }
+      if (tk)
+        fast_row_task<OP>(t, a, e, gb, tk, s_idx, s_slot, s_fl, s_off, src, dst, asrc, adst);
       wave_copy_pairs_q<U, 4>(src, dst, t.row_bytes, s_rows);
       if (OP == OP_ACCUM_OR_ASSIGN) wave_accum_pairs<U>(asrc, adst, t.row_bytes, a.value_type, s_rows);
     }
@@ -3788,9 +3779,50 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(8, 8))) 
   lds_barrier();
 
   /* W. Records and rows of the serial buckets; also of the others when
-        every wave held serial lanes (none was free to emit them above). */
-  emit_fast<OP, U, moves_rows>(t, a, m, part_b0, tid, kBlock, ns_w == kBlock / 64 ? 2 : 1, s_key,
-                           s_idx, s_sc, s_slot, s_fl, s_off, s_cnt, s_isser, s_rows[wv]);
+        every wave held serial lanes (none was free to emit them above).
+        The serial buckets' row tasks are listed first (in s_sc, whose
+        scores the records have consumed) and split evenly over the waves:
+        they are a few entries of the block, clustered by bucket, so a pass
+        over all entries would leave most lanes idle and some waves with
+        most of the rows. */
+  const uint8_t wser = ns_w == kBlock / 64 ? 2 : 1;
+  const bool wlist = moves_rows && wser == 1;
+  emit_fast<OP, U, moves_rows>(t, a, m, part_b0, tid, kBlock, wser, s_key, s_idx, s_sc, s_slot,
+                               s_fl, s_off, s_cnt, s_isser, s_rows[wv], !wlist);
+  if (wlist) {  // uniform in the block
+    __shared__ uint32_t s_nlist;
+    if (tid == 0) s_nlist = 0;
+    lds_barrier();
+    uint16_t* s_list = reinterpret_cast<uint16_t*>(s_sc);  // m <= kFastLds entries fit
+    for (uint32_t e0 = 0; e0 < m; e0 += kBlock) {
+      const uint32_t e = e0 + tid;
+      bool has = false;
+      if (e < m && (s_fl[e] & kTkMask)) {
+        const uint32_t lbk = (uint32_t)(bucket_of(t, s_key[e]) % kPartBuckets);
+        has = s_isser[lbk] == 1 && e - s_off[lbk] < s_cnt[lbk];
+      }
+      const uint64_t bm = __ballot(has);
+      uint32_t at = 0;
+      if (lane == 0 && bm) at = atomicAdd(&s_nlist, (uint32_t)__popcll(bm));
+      at = (uint32_t)__shfl((int)at, 0, 64);
+      if (has) s_list[at + __popcll(bm & ((1ull << lane) - 1))] = (uint16_t)e;
+    }
+    lds_barrier();
+    const uint32_t nl = s_nlist;
+    const uint32_t per = (nl + kBlock / 64 - 1) / (kBlock / 64);
+    const uint32_t j1 = min(nl, (wv + 1) * per);
+    for (uint32_t j = wv * per; j < j1; j += 64) {  // uniform in the wave
+      uint64_t src = 0, dst = 0, asrc = 0, adst = 0;
+      if (j + lane < j1) {
+        const uint32_t e = s_list[j + lane];
+        fast_row_task<OP>(t, a, e, bucket_of(t, s_key[e]), s_fl[e] & kTkMask, s_idx, s_slot,
+                          s_fl, s_off, src, dst, asrc, adst);
+      }
+      wave_copy_pairs_q<U, 4>(src, dst, t.row_bytes, s_rows[wv]);
+      if (OP == OP_ACCUM_OR_ASSIGN)
+        wave_accum_pairs<U>(asrc, adst, t.row_bytes, a.value_type, s_rows[wv]);
+    }
+  }
 #pragma unroll
   for (int d = 32; d > 0; d >>= 1) added += __shfl_xor(added, d, 64);
   if (lane == 0) s_wsum[wv] = added;
