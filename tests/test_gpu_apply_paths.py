@@ -290,3 +290,41 @@ def test_mixed_routes_in_one_call():
                            rng.integers(0, 1 << 30, ks.size, dtype=np.uint64))
         p.assert_same_state()
         p.assert_same_find(ks)
+
+
+@pytest.mark.parametrize("op", ["insert_or_assign", "find_or_insert"])
+@pytest.mark.parametrize("per_bucket,new_frac", [(1.5, 0.5), (2.5, 0.8)])
+def test_serial_bucket_rows_on_a_full_table(op, per_bucket, new_frac):
+    """A full 512-bucket table and batches of resident and new keys: every
+    bucket with a new key stops at it and hands the rest over, so the rows
+    of the resident keys before the stop are copied after the block barrier,
+    from the list of the serial buckets' row tasks (at 2.5 keys per bucket,
+    4 in 5 of them new, over 192 of a block's 256 buckets stop, every wave
+    holds serial lanes, and the block's last pass copies every row)."""
+    rng = np.random.default_rng(331 + int(per_bucket * 10))
+    cap, dim = 1 << 16, 32
+    p = Pair(cap, dim=dim, strategy=O.CUSTOMIZED)
+    resident = np.empty(0, np.uint64)
+    while p.g.load_factor() < 1.0:
+        ks = uniform_keys(rng, 2048, exclude=resident)
+        p.insert_or_assign(ks, rand_vals(rng, 2048, dim),
+                           rng.integers(1 << 20, 1 << 30, 2048, dtype=np.uint64))
+        resident = np.concatenate([resident, ks])
+    p.assert_same_state()
+    (gk, _, _), _ = p.export()
+    for b in range(3):
+        n = int(512 * per_bucket)
+        n_new = int(n * new_frac)
+        live = rng.choice(gk, n - n_new, replace=False)
+        new = uniform_keys(rng, n_new, exclude=resident)
+        resident = np.concatenate([resident, new])
+        ks = np.concatenate([live, new])
+        rng.shuffle(ks)
+        sc = rng.integers(1 << 30, 1 << 40, ks.size, dtype=np.uint64)
+        if op == "insert_or_assign":
+            p.insert_or_assign(ks, rand_vals(rng, ks.size, dim), sc)
+        else:
+            ov, gv = p.find_or_insert(ks, rand_vals(rng, ks.size, dim), sc)
+            np.testing.assert_array_equal(gv.view(np.uint8), ov.view(np.uint8))
+        p.assert_same_state()
+        (gk, _, _), _ = p.export()
