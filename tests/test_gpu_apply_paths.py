@@ -328,3 +328,23 @@ def test_serial_bucket_rows_on_a_full_table(op, per_bucket, new_frac):
             np.testing.assert_array_equal(gv.view(np.uint8), ov.view(np.uint8))
         p.assert_same_state()
         (gk, _, _), _ = p.export()
+
+
+def test_batches_over_2_20_keys():
+    """2^20 + 4096 keys per batch: 1028 chunks of 1024 keys, so the segment
+    scan keeps a column's counts in memory rather than in registers (more
+    than 32 chunks per thread); 8,000 entries per partition of a 2^23-slot
+    table take the multi-run kernel."""
+    rng = np.random.default_rng(341)
+    cap, dim, n = 1 << 23, 4, (1 << 20) + 4096
+    p = Pair(cap, dim=dim, strategy=O.CUSTOMIZED)
+    seen = np.empty(0, np.uint64)
+    for b in range(2):
+        ks = uniform_keys(rng, n, exclude=seen if b else None)
+        seen = np.concatenate([seen, ks])
+        p.insert_or_assign(ks, rand_vals(rng, n, dim),
+                           rng.integers(0, 1 << 40, n, dtype=np.uint64))
+        p.assert_same_state()
+    q = np.concatenate([rng.choice(seen, 4096, replace=False), uniform_keys(rng, 4096, exclude=seen)])
+    of = p.assert_same_find(q)
+    assert of.sum() == 4096
