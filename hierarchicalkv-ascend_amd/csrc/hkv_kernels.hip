@@ -1082,6 +1082,13 @@ __global__ __launch_bounds__(kBlock) void k_pcount(TableView t, const uint64_t* 
     ps.dctr[4] = 0;
     ps.dctr[5] = 0;
   }
+  // insert_and_evict flags a record per batch index; the flags of this
+  // batch start clear.  Chunk g's indices are words [32 g, 32 g + 32) of
+  // the bitmap, which holds n / 32 + 1 words.
+  if (ps.ev_bits && threadIdx.x < kPartChunk / 32) {
+    const uint64_t w = (uint64_t)g * (kPartChunk / 32) + threadIdx.x;
+    if (w <= n / 32) ps.ev_bits[w] = 0;
+  }
   uint32_t* H = ps.hist + (uint64_t)g * NP;
   for (uint32_t p0 = 0; p0 < NP; p0 += ps.prange) {
     const uint32_t w = NP - p0 < ps.prange ? NP - p0 : ps.prange;
@@ -2261,7 +2268,8 @@ __global__ __launch_bounds__(kBlock) void k_apply_part(TableView t, ApplyArgs a,
 // These kernels then produce the reference's compact output: with c records
 // in all, the k-th record at a position >= c moves into the k-th hole below
 // c (sources and destinations are disjoint, so every move runs in
-// parallel), the counter gets c, and the flags are cleared.
+// parallel), and the counter gets c.  The flags stay set until the next
+// call's k_pcount clears those of its own batch.
 /* ------------------------------------------------------------------------ */
 /* big partitions of batches with repeated keys                              */
 /* ------------------------------------------------------------------------ */
@@ -4979,7 +4987,6 @@ static void apply_part_op(const TableView& t, const ApplyArgs& a, const PartScra
     hipLaunchKernelGGL((k_evc_move<UU>), dim3(grid_for(a.n, kBlock, 2048)), b, 0, s,         \
                        ps.ev_bits, nw, ps.ev_wpre, ps.ev_blk, nbw, a.n, a.ev_keys,          \
                        a.ev_values, a.ev_scores, t.row_bytes);                               \
-    launch_fill_u32(ps.ev_bits, 0, nw, s);                                                   \
   }
   switch (a.unit) {
     case 16: HKV_PART_U(16); break;
